@@ -1,0 +1,180 @@
+"""Benchmark of the MI355X metal_linalg hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one synchronous C-ABI call over one batch of synthetic input that
+is already resident in HBM (torch tensors on cuda:0, passed as device
+pointers).  W untimed steps, then K timed steps between two
+synchronisations.  One JSON line on stdout: `value` = matrices/s over the
+timed steps; `roofline` = the dominant kernel's algorithmic bytes (or flops)
+per launch over its average duration, timed with HIP events on the
+library's launch stream during the timed steps; `cpu_baseline` = the oracle
+(the reference's LAPACK-batched CPU path restated) on the host's cores over
+a bounded sample of the same workload.
+
+Workloads are BASELINE.json's configs; the default is the one the headline
+metric is quoted on.  Data: synthetic, seeded (tests/_util.py generators).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+METRIC = "batched matrices/s (QR/eigh/SVD/chol/LU) + fp32 GFLOP/s & % peak at n=4096"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
+
+
+class Workload:
+    """name, inputs, the device call, and the accounting for one config."""
+
+    def __init__(self, name, desc, batch, make, call, kernel, bytes_per_call, flops_per_call, bound, oracle_call,
+                 shape):
+        self.name, self.desc, self.batch = name, desc, batch
+        self.make, self.call, self.kernel = make, call, kernel
+        self.bytes_per_call, self.flops_per_call, self.bound = bytes_per_call, flops_per_call, bound
+        self.oracle_call, self.shape = oracle_call, shape
+
+
+def workloads():
+    import _util as U
+
+    w = {}
+
+    def qr_make():
+        return {"a": U.config1_qr()}
+
+    def qr_call(api, t):
+        return api.qr(t["a"], "reduced")
+
+    w["qr"] = Workload(
+        "qr", "qr_with_mode reduced, 10000 x 32x32 fp32 N(0,1) (BASELINE config 1)", 10000, qr_make, qr_call,
+        "qr_small", 10000 * (3 * 32 * 32 * 4), 10000 * 87381, "hbm",
+        lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": 10000, "rows": 32, "cols": 32})
+    return w
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qr")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0, help="wall seconds of the CPU baseline sample")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              f"(the batch would shard across GPUs with no exchange, which no run here measures)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible; the library has no CPU path to measure", file=sys.stderr)
+        sys.exit(1)
+    from metal_linalg_amd import _lib, api
+
+    wl = workloads()[args.workload]
+    host = wl.make()
+    dev = {k: torch.from_numpy(np.ascontiguousarray(v)).to("cuda") for k, v in host.items()}
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        wl.call(api, dev)
+    torch.cuda.synchronize()
+
+    _lib.hip_reset_timing()
+    _lib.hip_set_timing(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.call(api, dev)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.hip_set_timing(0)
+
+    launches, kernel_ms = _lib.kernel_time(wl.kernel)
+    other = {n: _lib.kernel_time(n) for n in _lib.kernel_names()}
+    avg_kernel_s = (kernel_ms / 1e3) / max(launches, 1)
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = wl.batch * args.steps / elapsed
+
+    if wl.bound == "hbm":
+        achieved = wl.bytes_per_call / avg_kernel_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None}
+    else:
+        achieved = wl.flops_per_call / avg_kernel_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_MFMA_PEAK_TFS, 5), "traffic": None}
+    roof["kernel"] = wl.kernel
+    roof["kernel_avg_us"] = round(avg_kernel_s * 1e6, 3)
+    roof["launches"] = launches
+    roof["algorithmic_bytes_per_launch"] = wl.bytes_per_call
+    roof["algorithmic_flops_per_launch"] = wl.flops_per_call
+
+    # host-pointer (PCIe-inclusive) rate, for the record; never `value`
+    t0 = time.perf_counter()
+    reps = max(1, min(5, args.steps))
+    for _ in range(reps):
+        wl.call(api, host)
+    host_rate = wl.batch * reps / (time.perf_counter() - t0)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        import oracle
+
+        threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+        oracle.set_threads(threads)
+        n = wl.batch
+        wl.oracle_call(oracle, host, n)   # warm-up
+        count, t0 = 0, time.perf_counter()
+        while True:
+            wl.oracle_call(oracle, host, n)
+            count += n
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": round(count / cpu_s, 2), "unit": "matrices/s", "cores": oracle.threads(), "kind": "port",
+               "sample": f"{count} matrices ({count // n} passes over the full {wl.batch}-matrix batch) in "
+                         f"{cpu_s:.2f} s wall on {oracle.threads()} threads; {oracle.config()}"}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "matrices/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) per BASELINE.json configs; device-resident inputs)",
+        "config": dict({"workload": wl.desc}, **wl.shape),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "host_pointer_rate": round(host_rate, 2),
+        "kernels": {k: {"launches": v[0], "total_ms": round(v[1], 4)} for k, v in other.items()},
+        "device": _lib.device_name().decode(),
+        "arch": _lib.hip_arch().decode(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

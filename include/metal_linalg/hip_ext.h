@@ -1,0 +1,38 @@
+/* HIP-specific extensions of the MI355X build of metal_linalg.
+ *
+ * None of these has a counterpart in the reference library's C API; they
+ * exist for measurement (per-kernel HIP-event timing, read by bench.py) and
+ * for diagnostics.  Programs written against the reference never need them.
+ */
+#ifndef METAL_LINALG_HIP_EXT_H
+#define METAL_LINALG_HIP_EXT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Turn per-kernel timing on (1) or off (0).  While on, every kernel launch
+ * is bracketed by HIP events on the stream it is launched on, and the elapsed
+ * times are summed per kernel name when the call returns. */
+void metal_linalg_hip_set_timing(int on);
+
+/* Clear the per-kernel sums. */
+void metal_linalg_hip_reset_timing(void);
+
+/* Launch count and summed milliseconds of the kernel `name` since the last
+ * reset; returns 0 (and zeros) if it has not run. */
+int metal_linalg_hip_kernel_time(const char* name, uint64_t* launches, double* total_ms);
+
+/* The names of the kernels timed since the last reset, one per line. */
+const char* metal_linalg_hip_kernel_names(void);
+
+/* The device's gcnArchName ("" without a GPU). */
+const char* metal_linalg_hip_arch(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* METAL_LINALG_HIP_EXT_H */

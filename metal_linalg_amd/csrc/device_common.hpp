@@ -1,0 +1,56 @@
+// Device helpers shared by the kernels: lane-group reductions within a
+// wave64, the non-finite test and the quiet-NaN fill value.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cstdint>
+
+namespace mla {
+
+// The quiet NaN the reference writes for a non-finite matrix (0x7FC00000).
+__device__ __forceinline__ float qnan() { return __uint_as_float(0x7FC00000u); }
+
+// |v| <= FLT_MAX fails for NaN and for the infinities (the reference's scan,
+// src/metal_runtime.mm:161-162).
+__device__ __forceinline__ bool finite_f(float v) { return fabsf(v) <= FLT_MAX; }
+
+// Sum, max and or over an aligned group of G lanes (G a power of two <= 64),
+// the result on every lane of the group.
+template <int G>
+__device__ __forceinline__ float group_sum(float x) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, G);
+    return x;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float x) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, G));
+    return x;
+}
+
+template <int G>
+__device__ __forceinline__ int group_or(int x) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) x |= __shfl_xor(x, off, G);
+    return x;
+}
+
+// Power-of-two exponent e with amax * 2^-e in [0.5, 1) (frexp's), 0 for a
+// zero or non-finite amax: the reference's scaled_input rule
+// (src/metal_runtime.mm:179-215).
+__device__ __forceinline__ int scale_exponent(float amax) {
+    if (!(amax > 0.0f) || !(amax <= FLT_MAX)) return 0;
+    int e = 0;
+    (void)frexpf(amax, &e);
+    return e;
+}
+
+// A wave-level fence for LDS traffic between lanes of one wavefront: the
+// kernels that use it launch one wave per workgroup.
+__device__ __forceinline__ void wave_lds_sync() { __syncthreads(); }
+
+}  // namespace mla

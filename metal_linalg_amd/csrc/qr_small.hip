@@ -1,0 +1,180 @@
+// Batched Householder QR of small matrices (rows <= 64, columns <= 64), one
+// matrix per lane group of a wave64, held in registers.
+//
+// Role: the MI355X counterpart of the reference's qr_householder_simd
+// (reference: shaders/QR_Householder.metal:189-300, driver
+// src/qr_householder.mm:293-381): LAPACK's sgeqr2 + sorg2r per matrix, with
+// the reference GPU kernel's conventions -- the matrix scaled by a power of
+// two so that its largest entry lies in [0.5, 1), a reflector whose tail has
+// a sum of squares below 2^-80 taken as the identity, R unscaled on output,
+// and a matrix holding a NaN or an infinity written as all quiet NaN.
+//
+// Layout (MI355X-first, not the reference's): lane c of a G-lane group owns
+// column c of its matrix, all of its rows in VGPRs, so a column's dot
+// product with a reflector is a lane-local FMA chain and no cross-lane
+// reduction is needed; the reflector itself is broadcast through LDS.  A
+// row-major matrix read this way is coalesced: for a fixed row the group's
+// lanes read consecutive floats.  64/G matrices share a wave; one wave per
+// workgroup, so the LDS hand-offs need no s_barrier.
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mla {
+namespace {
+
+constexpr float kTinySumsq = 8.271806e-25f;   // 2^-80
+
+template <int G, int R>
+__global__ __launch_bounds__(64) void qr_small_kernel(const float* __restrict__ A, float* __restrict__ Q,
+                                                      float* __restrict__ Rout, uint32_t batch, uint32_t m,
+                                                      uint32_t n, uint32_t qc, uint32_t rr) {
+    constexpr int MPW = 64 / G;
+    __shared__ float vsh[MPW][R];
+    __shared__ float tsh[MPW][64];
+    const int lane = threadIdx.x;
+    const int c = lane % G;
+    const int g = lane / G;
+    const size_t mat = (size_t)blockIdx.x * MPW + g;
+    const bool live = mat < batch;
+    const int K = (int)(m < n ? m : n);
+
+    float x[R];
+    float amax = 0.0f;
+    int bad = 0;
+    const float* src = A + mat * m * n;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float v = 0.0f;
+        if (live && r < (int)m && c < (int)n) v = src[(size_t)r * n + c];
+        x[r] = v;
+        amax = fmaxf(amax, fabsf(v));
+        bad |= !finite_f(v);
+    }
+    amax = group_max<G>(amax);
+    bad = group_or<G>(bad);
+    const int e = bad ? 0 : scale_exponent(amax);
+#pragma unroll
+    for (int r = 0; r < R; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
+
+    // sgeqr2: column j's reflector H_j = I - tau v v^T, v(j) = 1
+    for (int j = 0; j < K; ++j) {
+        float ss = 0.0f, alpha = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ss = r > j ? fmaf(x[r], x[r], ss) : ss;
+            alpha = r == j ? x[r] : alpha;
+        }
+        float beta = alpha, tau = 0.0f, scale = 1.0f;
+        if (ss >= kTinySumsq) {
+            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
+            tau = (beta - alpha) / beta;
+            scale = 1.0f / (alpha - beta);
+        }
+        if (c == j) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float v = r < j ? 0.0f : (r == j ? 1.0f : x[r] * scale);
+                vsh[g][r] = v;
+                x[r] = r == j ? beta : (r > j ? v : x[r]);
+            }
+            tsh[g][j] = tau;
+        }
+        wave_lds_sync();
+        if (c > j) {
+            const float t = tsh[g][j];
+            float d = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) d = r >= j ? fmaf(vsh[g][r], x[r], d) : d;
+            d *= t;
+#pragma unroll
+            for (int r = 0; r < R; ++r) x[r] = r >= j ? fmaf(-d, vsh[g][r], x[r]) : x[r];
+        }
+        wave_lds_sync();
+    }
+
+    // R: rows below K are zero (complete mode), the strict lower part zero
+    if (live) {
+        float* out_r = Rout + mat * rr * n;
+        const float unscale = ldexpf(1.0f, e);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < (int)rr && c < (int)n) {
+                float v = (r < K && c >= r) ? x[r] * unscale : 0.0f;
+                out_r[(size_t)r * n + c] = bad ? qnan() : v;
+            }
+        }
+    }
+    if (qc == 0) return;
+
+    // sorg2r backward: columns >= K of a square Q start as the identity's
+    if (c >= K) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) x[r] = r == c ? 1.0f : 0.0f;
+    }
+    for (int j = K - 1; j >= 0; --j) {
+        if (c == j) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) vsh[g][r] = r < j ? 0.0f : (r == j ? 1.0f : x[r]);
+        }
+        wave_lds_sync();
+        const float t = tsh[g][j];
+        if (c > j && c < (int)qc) {
+            float d = 0.0f;
+#pragma unroll
+            for (int r = 0; r < R; ++r) d = r >= j ? fmaf(vsh[g][r], x[r], d) : d;
+            d *= t;
+#pragma unroll
+            for (int r = 0; r < R; ++r) x[r] = r >= j ? fmaf(-d, vsh[g][r], x[r]) : x[r];
+        } else if (c == j) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) x[r] = r < j ? 0.0f : (r == j ? 1.0f - t : -t * x[r]);
+        }
+        wave_lds_sync();
+    }
+    if (live && c < (int)qc) {
+        float* out_q = Q + mat * m * qc;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r < (int)m) out_q[(size_t)r * qc + c] = bad ? qnan() : x[r];
+    }
+}
+
+template <int G, int R>
+void launch_g_r(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
+                hipStream_t s) {
+    constexpr int MPW = 64 / G;
+    const uint64_t blocks = cdiv(batch, MPW);
+    KernelTimer t("qr_small", s);
+    hipLaunchKernelGGL((qr_small_kernel<G, R>), dim3((uint32_t)blocks), dim3(64), 0, s, a, q, r, batch, m, n, qc, rr);
+    t.stop();
+}
+
+template <int G>
+void launch_g(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
+              hipStream_t s) {
+    if (m <= 8) launch_g_r<G, 8>(a, q, r, batch, m, n, qc, rr, s);
+    else if (m <= 16) launch_g_r<G, 16>(a, q, r, batch, m, n, qc, rr, s);
+    else if (m <= 32) launch_g_r<G, 32>(a, q, r, batch, m, n, qc, rr, s);
+    else launch_g_r<G, 64>(a, q, r, batch, m, n, qc, rr, s);
+}
+
+}  // namespace
+
+bool qr_small_fits(uint32_t m, uint32_t n, uint32_t qc) {
+    return m <= 64 && n <= 64 && qc <= 64 && m >= 1 && n >= 1;
+}
+
+void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
+              hipStream_t s) {
+    if (!qr_small_fits(m, n, qc)) invalid("[qr] qr_small takes at most 64 rows and 64 columns");
+    if (batch == 0) return;
+    const uint32_t w = n > qc ? n : qc;
+    if (w <= 8) launch_g<8>(a, q, r, batch, m, n, qc, rr, s);
+    else if (w <= 16) launch_g<16>(a, q, r, batch, m, n, qc, rr, s);
+    else if (w <= 32) launch_g<32>(a, q, r, batch, m, n, qc, rr, s);
+    else launch_g<64>(a, q, r, batch, m, n, qc, rr, s);
+    MLA_HIP(hipGetLastError());
+}
+
+}  // namespace mla
