@@ -140,6 +140,145 @@ __global__ __launch_bounds__(64) void qr_small_kernel(const float* __restrict__ 
     }
 }
 
+// Sum of x[r] * y[r] for r in [lo, M), four partial sums to shorten the
+// dependent FMA chain; everything compile-time.
+template <int LO, int M>
+__device__ __forceinline__ float dot_from(const float* x, const float* y) {
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+    for (int r = LO; r < M; r += 4) {
+        s0 = fmaf(x[r], y[r], s0);
+        if (r + 1 < M) s1 = fmaf(x[r + 1], y[r + 1], s1);
+        if (r + 2 < M) s2 = fmaf(x[r + 2], y[r + 2], s2);
+        if (r + 3 < M) s3 = fmaf(x[r + 3], y[r + 3], s3);
+    }
+    return (s0 + s1) + (s2 + s3);
+}
+
+// Factorization step J of the fixed-shape kernel (compile-time J, so every
+// row predicate folds away and only rows >= J are touched).
+template <int J, int M, int N, int G, int LD>
+__device__ __forceinline__ void qr_fixed_step(float (&x)[M], float (&vsh)[LD], float* tsh, int c) {
+    if constexpr (J < (M < N ? M : N)) {
+        float ss = dot_from<J + 1, M>(x, x);
+        const float alpha = x[J];
+        float beta = alpha, tau = 0.0f, scale = 1.0f;
+        if (ss >= kTinySumsq) {
+            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
+            tau = (beta - alpha) / beta;
+            scale = 1.0f / (alpha - beta);
+        }
+        if (c == J) {
+            x[J] = beta;
+#pragma unroll
+            for (int r = J + 1; r < M; ++r) {
+                x[r] *= scale;
+                vsh[r] = x[r];
+            }
+            vsh[J] = 1.0f;
+            tsh[J] = tau;
+        }
+        wave_lds_sync();
+        if (c > J) {
+            float v[M];
+#pragma unroll
+            for (int r = J; r < M; ++r) v[r] = vsh[r];
+            const float d = tsh[J] * dot_from<J, M>(v, x);
+#pragma unroll
+            for (int r = J; r < M; ++r) x[r] = fmaf(-d, v[r], x[r]);
+        }
+        wave_lds_sync();
+        qr_fixed_step<J + 1, M, N, G, LD>(x, vsh, tsh, c);
+    }
+}
+
+// Q formation step J (backward, sorg2r), for J = K-1 down to 0.
+template <int J, int M, int K, int LD>
+__device__ __forceinline__ void qr_fixed_qstep(float (&x)[M], float (&vsh)[LD], const float* tsh, int c, int qc) {
+    if constexpr (J >= 0) {
+        if (c == J) {
+            vsh[J] = 1.0f;
+#pragma unroll
+            for (int r = J + 1; r < M; ++r) vsh[r] = x[r];
+        }
+        wave_lds_sync();
+        const float t = tsh[J];
+        if (c > J && c < qc) {
+            float v[M];
+#pragma unroll
+            for (int r = J; r < M; ++r) v[r] = vsh[r];
+            const float d = t * dot_from<J, M>(v, x);
+#pragma unroll
+            for (int r = J; r < M; ++r) x[r] = fmaf(-d, v[r], x[r]);
+        } else if (c == J) {
+#pragma unroll
+            for (int r = 0; r < M; ++r) x[r] = r < J ? 0.0f : (r == J ? 1.0f - t : -t * x[r]);
+        }
+        wave_lds_sync();
+        qr_fixed_qstep<J - 1, M, K, LD>(x, vsh, tsh, c, qc);
+    }
+}
+
+// Fixed-shape variant for M >= N known at compile time (the hot batched
+// shapes): the column loop is unrolled, so row predicates vanish and step j
+// touches rows j.. only.  qc is 0 (R alone) or N.
+template <int M, int N, int G>
+__global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ A, float* __restrict__ Q,
+                                                      float* __restrict__ Rout, uint32_t batch, uint32_t qc) {
+    constexpr int MPW = 64 / G;
+    constexpr int LD = M + 4;   // per-group stride, off the other group's banks
+    __shared__ float vsh[MPW][LD];
+    __shared__ float tsh[MPW][N];
+    const int lane = threadIdx.x;
+    const int c = lane % G;
+    const int g = lane / G;
+    const size_t mat = (size_t)blockIdx.x * MPW + g;
+    const bool live = mat < batch;
+
+    float x[M];
+    float amax = 0.0f;
+    int bad = 0;
+    const float* src = A + mat * M * N;
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+        float v = 0.0f;
+        if (live && c < N) v = src[(size_t)r * N + c];
+        x[r] = v;
+        amax = fmaxf(amax, fabsf(v));
+        bad |= !finite_f(v);
+    }
+    amax = group_max<G>(amax);
+    bad = group_or<G>(bad);
+    const int e = bad ? 0 : scale_exponent(amax);
+#pragma unroll
+    for (int r = 0; r < M; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
+
+    qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], c);
+
+    if (live && c < N) {
+        float* out_r = Rout + mat * N * N;
+        const float unscale = ldexpf(1.0f, e);
+#pragma unroll
+        for (int r = 0; r < N; ++r) out_r[(size_t)r * N + c] = bad ? qnan() : (c >= r ? x[r] * unscale : 0.0f);
+    }
+    if (qc == 0) return;
+    qr_fixed_qstep<N - 1, M, N, LD>(x, vsh[g], tsh[g], c, (int)qc);
+    if (live && c < N) {
+        float* out_q = Q + mat * M * N;
+#pragma unroll
+        for (int r = 0; r < M; ++r) out_q[(size_t)r * N + c] = bad ? qnan() : x[r];
+    }
+}
+
+template <int M, int N, int G>
+void launch_fixed(const float* a, float* q, float* r, uint32_t batch, uint32_t qc, hipStream_t s) {
+    constexpr int MPW = 64 / G;
+    KernelTimer t("qr_small", s);
+    hipLaunchKernelGGL((qr_fixed_kernel<M, N, G>), dim3((uint32_t)cdiv(batch, MPW)), dim3(64), 0, s, a, q, r, batch,
+                       qc);
+    t.stop();
+}
+
 template <int G, int R>
 void launch_g_r(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
                 hipStream_t s) {
@@ -169,6 +308,15 @@ void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, ui
               hipStream_t s) {
     if (!qr_small_fits(m, n, qc)) invalid("[qr] qr_small takes at most 64 rows and 64 columns");
     if (batch == 0) return;
+    if (m == n && (qc == 0 || qc == n) && rr == n) {
+        switch (n) {
+            case 8: launch_fixed<8, 8, 8>(a, q, r, batch, qc, s); MLA_HIP(hipGetLastError()); return;
+            case 16: launch_fixed<16, 16, 16>(a, q, r, batch, qc, s); MLA_HIP(hipGetLastError()); return;
+            case 32: launch_fixed<32, 32, 32>(a, q, r, batch, qc, s); MLA_HIP(hipGetLastError()); return;
+            case 64: launch_fixed<64, 64, 64>(a, q, r, batch, qc, s); MLA_HIP(hipGetLastError()); return;
+            default: break;
+        }
+    }
     const uint32_t w = n > qc ? n : qc;
     if (w <= 8) launch_g<8>(a, q, r, batch, m, n, qc, rr, s);
     else if (w <= 16) launch_g<16>(a, q, r, batch, m, n, qc, rr, s);
