@@ -61,6 +61,34 @@ def workloads():
         "qr", "qr_with_mode reduced, 10000 x 32x32 fp32 N(0,1) (BASELINE config 1)", 10000, qr_make, qr_call,
         "qr_small", 10000 * (3 * 32 * 32 * 4), 10000 * 87381, "hbm",
         lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": 10000, "rows": 32, "cols": 32})
+
+    def chol_make():
+        a, _ = U.config4_spd()
+        return {"a": a}
+
+    w["cholesky"] = Workload(
+        "cholesky", "cholesky lower, 8192 x 16x16 SPD fp32, 1% non-SPD (BASELINE config 4)", 8192, chol_make,
+        lambda api, t: api.cholesky(t["a"], False), "chol_small", 8192 * (1024 + 1024 + 4), 8192 * 1365, "hbm",
+        lambda o, h, n: o.cholesky(h["a"][:n], False), {"batch": 8192, "n": 16})
+
+    def lu_make():
+        a, b = U.config4_lu()
+        return {"a": a, "b": b}
+
+    w["lu"] = Workload(
+        "lu", "lu_factor, 8192 x 16x16 fp32 N(0,1) (BASELINE config 4)", 8192, lu_make,
+        lambda api, t: api.lu_factor(t["a"]), "lu_small_factor", 8192 * (1024 + 1024 + 64 + 4), 8192 * 2731, "hbm",
+        lambda o, h, n: o.lu_factor(h["a"][:n]), {"batch": 8192, "n": 16})
+    w["solve"] = Workload(
+        "solve", "solve, 8192 x 16x16 fp32 with 4 right-hand sides (BASELINE config 4)", 8192, lu_make,
+        lambda api, t: api.solve(t["a"], t["b"]), "lu_small_solve", 8192 * (1024 + 256 + 256 + 4),
+        8192 * (2731 + 2 * 16 * 16 * 4), "hbm",
+        lambda o, h, n: o.solve(h["a"][:n], h["b"][:n]), {"batch": 8192, "n": 16, "nrhs": 4})
+    w["trsm"] = Workload(
+        "trsm", "solve_triangular lower unit, 8192 x 16x16 fp32, 4 right-hand sides (BASELINE config 4)", 8192,
+        lu_make, lambda api, t: api.solve_triangular(t["a"], t["b"], False, True), "trsm_small",
+        8192 * (1024 + 256 + 256), 8192 * 1024, "hbm",
+        lambda o, h, n: o.solve_triangular(h["a"][:n], h["b"][:n], False, True), {"batch": 8192, "n": 16, "nrhs": 4})
     return w
 
 

@@ -78,29 +78,102 @@ void svd(const Matrices&, float*, float*, float*, uint32_t*) {
     invalid("[svd] not available in this build yet");
 }
 
-void cholesky(const Matrices&, bool, float*, uint32_t*) {
+namespace {
+
+void require_square(const Matrices& a, const char* what) {
+    if (a.rows != a.cols)
+        invalid(std::string("[") + what + "] The matrices must be square, got " + std::to_string(a.rows) + "x" +
+                std::to_string(a.cols) + ".");
+}
+
+[[noreturn]] void too_large(const char* what, uint32_t n) {
+    invalid(std::string("[") + what + "] n = " + std::to_string(n) +
+            ": this build's kernels for this decomposition take n <= 32 so far");
+}
+
+}  // namespace
+
+// reference: src/cholesky.mm:178-189 (core::cholesky)
+void cholesky(const Matrices& a, bool upper, float* l, uint32_t* info) {
     require_gpu_allowed("cholesky");
-    invalid("[cholesky] not available in this build yet");
+    require_square(a, "cholesky");
+    const uint32_t n = a.cols, B = a.batch;
+    if (n == 0 || B == 0) return;
+    if (!chol_small_fits(n)) too_large("cholesky", n);
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    float* dl = call.out(l, (size_t)B * n * n);
+    uint32_t* di = call.out(info, B);
+    chol_small(da, dl, di, B, n, upper, call.stream());
+    call.finish();
 }
 
-void lu_factor(const Matrices&, float*, uint32_t*, uint32_t*) {
+// reference: src/lu.mm:148-166 (core::lu_factor, solve, inv)
+void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
     require_gpu_allowed("lu_factor");
-    invalid("[lu_factor] not available in this build yet");
+    require_square(a, "lu_factor");
+    const uint32_t n = a.cols, B = a.batch;
+    if (n == 0 || B == 0) return;
+    if (!lu_small_fits(n)) too_large("lu_factor", n);
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    float* dlu = call.out(lu, (size_t)B * n * n);
+    uint32_t* dp = call.out(pivots, (size_t)B * n);
+    uint32_t* di = call.out(info, B);
+    lu_small_factor(da, dlu, dp, di, B, n, call.stream());
+    call.finish();
 }
 
-void solve(const Matrices&, const float*, uint32_t, float*, uint32_t*) {
+void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t* info) {
     require_gpu_allowed("solve");
-    invalid("[solve] not available in this build yet");
+    require_square(a, "solve");
+    const uint32_t n = a.cols, B = a.batch;
+    if (n == 0 || B == 0 || nrhs == 0) {
+        if (info && B) {   // reference: lu_cpu.mm:108-111 (info zeroed)
+            Call call;
+            uint32_t* di = call.out(info, B);
+            MLA_HIP(hipMemsetAsync(di, 0, (size_t)B * sizeof(uint32_t), call.stream()));
+            call.finish();
+        }
+        return;
+    }
+    if (!lu_small_fits(n)) too_large("solve", n);
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    const float* db = call.in(b, (size_t)B * n * nrhs);
+    float* dx = call.out(x, (size_t)B * n * nrhs);
+    uint32_t* di = call.out(info, B);
+    lu_small_solve(da, db, nrhs, dx, di, B, n, call.stream());
+    call.finish();
 }
 
-void inv(const Matrices&, float*, uint32_t*) {
+void inv(const Matrices& a, float* x, uint32_t* info) {
     require_gpu_allowed("inv");
-    invalid("[inv] not available in this build yet");
+    require_square(a, "inv");
+    const uint32_t n = a.cols, B = a.batch;
+    if (n == 0 || B == 0) return;
+    if (!lu_small_fits(n)) too_large("inv", n);
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    float* dx = call.out(x, (size_t)B * n * n);
+    uint32_t* di = call.out(info, B);
+    lu_small_inv(da, dx, di, B, n, call.stream());
+    call.finish();
 }
 
-void solve_triangular(const Matrices&, const float*, uint32_t, bool, bool, float*) {
+// reference: src/trsm.mm:288-294 (core::solve_triangular)
+void solve_triangular(const Matrices& a, const float* b, uint32_t nrhs, bool upper, bool unit, float* x) {
     require_gpu_allowed("solve_triangular");
-    invalid("[solve_triangular] not available in this build yet");
+    require_square(a, "solve_triangular");
+    const uint32_t n = a.cols, B = a.batch;
+    if (n == 0 || B == 0 || nrhs == 0) return;
+    if (!lu_small_fits(n)) too_large("solve_triangular", n);
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    const float* db = call.in(b, (size_t)B * n * nrhs);
+    float* dx = call.out(x, (size_t)B * n * nrhs);
+    trsm_small(da, db, dx, B, n, nrhs, upper, unit, call.stream());
+    call.finish();
 }
 
 }  // namespace mla::core

@@ -15,4 +15,18 @@ bool qr_small_fits(uint32_t m, uint32_t n, uint32_t qc);
 void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
               hipStream_t s);
 
+// ---- Cholesky, n <= 32 ----
+bool chol_small_fits(uint32_t n);
+void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s);
+
+// ---- LU, solve, inverse, triangular solve, n <= 32 ----
+bool lu_small_fits(uint32_t n);
+void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
+                     hipStream_t s);
+void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, uint32_t batch,
+                    uint32_t n, hipStream_t s);
+void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint32_t n, hipStream_t s);
+void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
+                bool unit, hipStream_t s);
+
 }  // namespace mla

@@ -1,0 +1,306 @@
+// Batched LU with partial pivoting, solve, inverse and triangular solve for
+// small matrices (n <= 32), one matrix per lane group of a wave64, in
+// registers.
+//
+// Role: the reference has no batched-small GPU LU or TRSM; its CPU path is
+// the contract (reference: src/lu_cpu.mm:72-157, src/trsm.mm:193-206):
+// sgetrf's partial pivoting (the first entry of largest magnitude, 0-based
+// sequential swaps in `pivots`), info = k for the first exactly-zero U(k-1,
+// k-1) with the factorization completed, and for solve/inv a singular
+// matrix's x all NaN; strsm's substitution reading one triangle, with a unit
+// diagonal not read.
+//
+// Layout: lane c of a group owns column c of [A | B], A's columns first
+// (n padded to a power of two N with the identity), the right-hand sides
+// after them (inv: the identity's columns).  At elimination step k lane k
+// picks the pivot row from its own column, forms the multipliers and
+// broadcasts both through LDS; every lane swaps the two rows in its column
+// and updates it.  Back substitution then reads U from LDS.  Right-hand
+// sides beyond one group's width are split over blockIdx.y.
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mla {
+namespace {
+
+enum Mode { kFactor = 0, kSolve = 1, kInv = 2 };
+
+constexpr float kSfmin = 1.17549435e-38f;   // FLT_MIN: sgetf2 divides below it
+
+// x[k] <-> x[p] for a runtime p >= k (a select chain: the row index must stay
+// a compile-time register index).
+template <int K, int N>
+__device__ __forceinline__ void swap_rows(float (&x)[N], int p) {
+    const float xk = x[K];
+    float xp = xk;
+#pragma unroll
+    for (int r = K + 1; r < N; ++r) xp = (r == p) ? x[r] : xp;
+#pragma unroll
+    for (int r = K + 1; r < N; ++r) x[r] = (r == p) ? xk : x[r];
+    x[K] = xp;
+}
+
+template <int K, int N>
+__device__ __forceinline__ void lu_step(float (&x)[N], float* col, int* pivsh, int c, int n, int& info,
+                                        int& mypiv) {
+    if constexpr (K < N) {
+        if (c == K) {
+            float best = fabsf(x[K]);
+            int p = K;
+#pragma unroll
+            for (int r = K + 1; r < N; ++r) {
+                const float a = fabsf(x[r]);
+                if (a > best) {
+                    best = a;
+                    p = r;
+                }
+            }
+            swap_rows<K, N>(x, p);
+            const float piv = x[K];
+            if (piv != 0.0f) {
+                if (fabsf(piv) >= kSfmin) {
+                    const float inv = 1.0f / piv;
+#pragma unroll
+                    for (int r = K + 1; r < N; ++r) x[r] *= inv;
+                } else {
+#pragma unroll
+                    for (int r = K + 1; r < N; ++r) x[r] /= piv;
+                }
+            }
+#pragma unroll
+            for (int r = K + 1; r < N; ++r) col[r] = x[r];
+            pivsh[K] = p;
+            pivsh[N + K] = piv == 0.0f ? 1 : 0;
+            mypiv = p;
+        }
+        wave_lds_sync();
+        const int p = pivsh[K];
+        if (info == 0 && K < n && pivsh[N + K] != 0) info = K + 1;
+        if (c != K) {
+            swap_rows<K, N>(x, p);
+            if (c > K) {
+                const float f = x[K];
+#pragma unroll
+                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-col[r], f, x[r]);
+            }
+        }
+        wave_lds_sync();
+        lu_step<K + 1, N>(x, col, pivsh, c, n, info, mypiv);
+    }
+}
+
+// G = N lanes (factor) or 2N (A's N columns, then up to N right-hand sides).
+template <int N, int MODE>
+__global__ __launch_bounds__(64) void lu_small_kernel(const float* __restrict__ A, float* __restrict__ LU,
+                                                      uint32_t* __restrict__ pivots, uint32_t* __restrict__ info_out,
+                                                      const float* __restrict__ B, float* __restrict__ X,
+                                                      uint32_t batch, uint32_t n, uint32_t nrhs) {
+    constexpr int G = MODE == kFactor ? N : 2 * N;
+    constexpr int MPW = 64 / G;
+    __shared__ float col[MPW][N + 4];
+    __shared__ int pivsh[MPW][2 * N];
+    __shared__ float ush[MODE == kFactor ? 1 : MPW][MODE == kFactor ? 1 : N][N + 1];
+    const int lane = threadIdx.x;
+    const int c = lane % G;
+    const int g = lane / G;
+    const size_t mat = (size_t)blockIdx.x * MPW + g;
+    const bool live = mat < batch;
+    const int rc = c - N;                                   // right-hand-side column of this lane (if >= 0)
+    const int col0 = (int)blockIdx.y * N;                   // first right-hand side of this block
+    const int nr = MODE == kInv ? (int)n : (int)nrhs;
+    const bool rhs_lane = MODE != kFactor && rc >= 0 && col0 + rc < nr;
+    const size_t per = (size_t)n * n;
+
+    float x[N];
+    const float* src = A + mat * per;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        float v = 0.0f;
+        if (c < N) {
+            v = (r == c) ? 1.0f : 0.0f;   // identity padding
+            if (live && c < (int)n && r < (int)n) v = src[(size_t)r * n + c];
+        } else if (rhs_lane && r < (int)n) {
+            if (MODE == kInv) v = (r == col0 + rc) ? 1.0f : 0.0f;
+            else if (live) v = B[mat * (size_t)n * nrhs + (size_t)r * nrhs + col0 + rc];
+        }
+        x[r] = v;
+    }
+
+    int info = 0, mypiv = 0;
+    lu_step<0, N>(x, col[g], pivsh[g], c, (int)n, info, mypiv);
+
+    if constexpr (MODE == kFactor) {
+        if (!live) return;
+        if (info_out && c == 0) info_out[mat] = (uint32_t)info;
+        if (c >= (int)n) return;
+        pivots[mat * n + c] = (uint32_t)mypiv;
+        float* dst = LU + mat * per;
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+            if (r < (int)n) dst[(size_t)r * n + c] = x[r];
+    } else {
+        if (c < N) {
+#pragma unroll
+            for (int r = 0; r < N; ++r) ush[g][r][c] = x[r];
+        }
+        wave_lds_sync();
+        if (rhs_lane) {
+#pragma unroll
+            for (int k = N - 1; k >= 0; --k) {
+                const float y = x[k] / ush[g][k][k];
+                x[k] = y;
+#pragma unroll
+                for (int r = 0; r < k; ++r) x[r] = fmaf(-ush[g][r][k], y, x[r]);
+            }
+        }
+        if (!live) return;
+        if (info_out && c == 0 && blockIdx.y == 0) info_out[mat] = (uint32_t)info;
+        if (!rhs_lane) return;
+        const int ld = MODE == kInv ? (int)n : (int)nrhs;
+        float* dst = X + mat * (size_t)n * ld;
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+            if (r < (int)n) dst[(size_t)r * ld + col0 + rc] = info ? qnan() : x[r];
+    }
+}
+
+// Triangular solve: lanes [0, N) hold the triangle's columns (identity
+// padded, unit diagonal as 1, the other triangle never read), lanes
+// [N, 2N) the right-hand sides.
+template <int N>
+__global__ __launch_bounds__(64) void trsm_small_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                        float* __restrict__ X, uint32_t batch, uint32_t n,
+                                                        uint32_t nrhs, int upper, int unit) {
+    constexpr int G = 2 * N;
+    constexpr int MPW = 64 / G;
+    __shared__ float tsh[MPW][N][N + 1];
+    const int lane = threadIdx.x;
+    const int c = lane % G;
+    const int g = lane / G;
+    const size_t mat = (size_t)blockIdx.x * MPW + g;
+    const bool live = mat < batch;
+    const int rc = c - N;
+    const int col0 = (int)blockIdx.y * N;
+    const bool rhs_lane = rc >= 0 && col0 + rc < (int)nrhs;
+    const size_t per = (size_t)n * n;
+
+    if (c < N) {
+        const float* src = A + mat * per;
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            float v = (r == c) ? 1.0f : 0.0f;
+            if (live && c < (int)n && r < (int)n) {
+                const bool in = upper ? r < c : r > c;   // strictly inside the triangle
+                if (in) v = src[(size_t)r * n + c];
+                else if (r == c) v = unit ? 1.0f : src[(size_t)r * n + c];
+                else v = 0.0f;
+            }
+            tsh[g][r][c] = v;
+        }
+    }
+    float y[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+        y[r] = (live && rhs_lane && r < (int)n) ? B[mat * (size_t)n * nrhs + (size_t)r * nrhs + col0 + rc] : 0.0f;
+    wave_lds_sync();
+    if (rhs_lane) {
+        if (upper) {
+#pragma unroll
+            for (int k = N - 1; k >= 0; --k) {
+                const float v = y[k] / tsh[g][k][k];
+                y[k] = v;
+#pragma unroll
+                for (int r = 0; r < k; ++r) y[r] = fmaf(-tsh[g][r][k], v, y[r]);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const float v = y[k] / tsh[g][k][k];
+                y[k] = v;
+#pragma unroll
+                for (int r = k + 1; r < N; ++r) y[r] = fmaf(-tsh[g][r][k], v, y[r]);
+            }
+        }
+    }
+    if (!live || !rhs_lane) return;
+    float* dst = X + mat * (size_t)n * nrhs;
+#pragma unroll
+    for (int r = 0; r < N; ++r)
+        if (r < (int)n) dst[(size_t)r * nrhs + col0 + rc] = y[r];
+}
+
+template <int N, int MODE>
+void launch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const float* b, float* x, uint32_t batch,
+               uint32_t n, uint32_t nrhs, hipStream_t s, const char* name) {
+    constexpr int G = MODE == kFactor ? N : 2 * N;
+    constexpr int MPW = 64 / G;
+    const uint32_t chunks = MODE == kSolve ? (uint32_t)cdiv(nrhs, N) : 1;
+    KernelTimer t(name, s);
+    hipLaunchKernelGGL((lu_small_kernel<N, MODE>), dim3((uint32_t)cdiv(batch, MPW), chunks), dim3(64), 0, s, a, lu,
+                       piv, info, b, x, batch, n, nrhs);
+    t.stop();
+}
+
+template <int MODE>
+void dispatch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const float* b, float* x, uint32_t batch,
+                 uint32_t n, uint32_t nrhs, hipStream_t s, const char* name) {
+    if (n <= 4) launch_lu<4, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else if (n <= 8) launch_lu<8, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else if (n <= 16) launch_lu<16, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else launch_lu<32, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    MLA_HIP(hipGetLastError());
+}
+
+template <int N>
+void launch_trsm(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
+                 bool unit, hipStream_t s) {
+    constexpr int MPW = 64 / (2 * N);
+    KernelTimer t("trsm_small", s);
+    hipLaunchKernelGGL((trsm_small_kernel<N>), dim3((uint32_t)cdiv(batch, MPW), (uint32_t)cdiv(nrhs, N)), dim3(64),
+                       0, s, a, b, x, batch, n, nrhs, upper ? 1 : 0, unit ? 1 : 0);
+    t.stop();
+}
+
+constexpr uint32_t kMaxGridY = 65535;
+
+}  // namespace
+
+bool lu_small_fits(uint32_t n) { return n >= 1 && n <= 32; }
+
+void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
+                     hipStream_t s) {
+    if (!lu_small_fits(n)) invalid("[lu_factor] lu_small takes n <= 32");
+    if (batch == 0) return;
+    dispatch_lu<kFactor>(a, lu, pivots, info, nullptr, nullptr, batch, n, 0, s, "lu_small_factor");
+}
+
+void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, uint32_t batch,
+                    uint32_t n, hipStream_t s) {
+    if (!lu_small_fits(n)) invalid("[solve] lu_small takes n <= 32");
+    if (batch == 0 || nrhs == 0) return;
+    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : 32;
+    if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve] too many right-hand sides for one call");
+    dispatch_lu<kSolve>(a, nullptr, nullptr, info, b, x, batch, n, nrhs, s, "lu_small_solve");
+}
+
+void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint32_t n, hipStream_t s) {
+    if (!lu_small_fits(n)) invalid("[inv] lu_small takes n <= 32");
+    if (batch == 0) return;
+    dispatch_lu<kInv>(a, nullptr, nullptr, info, nullptr, x, batch, n, n, s, "lu_small_inv");
+}
+
+void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
+                bool unit, hipStream_t s) {
+    if (!lu_small_fits(n)) invalid("[solve_triangular] trsm_small takes n <= 32");
+    if (batch == 0 || nrhs == 0) return;
+    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : 32;
+    if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve_triangular] too many right-hand sides for one call");
+    if (n <= 4) launch_trsm<4>(a, b, x, batch, n, nrhs, upper, unit, s);
+    else if (n <= 8) launch_trsm<8>(a, b, x, batch, n, nrhs, upper, unit, s);
+    else if (n <= 16) launch_trsm<16>(a, b, x, batch, n, nrhs, upper, unit, s);
+    else launch_trsm<32>(a, b, x, batch, n, nrhs, upper, unit, s);
+    MLA_HIP(hipGetLastError());
+}
+
+}  // namespace mla
