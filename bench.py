@@ -62,6 +62,16 @@ def workloads():
         "qr_small", 10000 * (3 * 32 * 32 * 4), 10000 * 87381, "hbm",
         lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": 10000, "rows": 32, "cols": 32})
 
+    def eigh_make():
+        return {"a": U.config2_eigh()}
+
+    w["eigh"] = Workload(
+        "eigh", "eigh lower with vectors, 4096 x 64x64 fp32 symmetric, 10% scaled by 10^U(-30,37), "
+                "one NaN matrix (BASELINE config 2)", 4096, eigh_make,
+        lambda api, t: api.eigh(t["a"], True, True), "eigh_small", 4096 * (16384 + 256 + 16384 + 4),
+        4096 * 9 * 64 ** 3, "hbm",
+        lambda o, h, n: o.eigh(h["a"][:n], True, True), {"batch": 4096, "n": 64})
+
     def chol_make():
         a, _ = U.config4_spd()
         return {"a": a}
@@ -97,7 +107,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="qr")
+    ap.add_argument("--workload", default="eigh")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=2.0, help="wall seconds of the CPU baseline sample")
     args = ap.parse_args()

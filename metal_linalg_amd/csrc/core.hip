@@ -68,9 +68,51 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
     call.finish();
 }
 
-void eigh(const Matrices&, bool, float*, float*, uint32_t*) {
+namespace {
+
+// A finite matrix that did not converge is an error (reference:
+// src/eigh_ql.mm:254-262, src/svd_golub_kahan.mm:349-362): the info words
+// are read back and checked.
+void check_converged(const uint32_t* dinfo, uint32_t batch, hipStream_t s, const char* what) {
+    std::vector<uint32_t> h(batch);
+    MLA_HIP(hipMemcpyAsync(h.data(), dinfo, (size_t)batch * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    MLA_HIP(hipStreamSynchronize(s));
+    for (uint32_t b = 0; b < batch; ++b) {
+        const uint32_t i = h[b];
+        if (!((i >> 17) & 1u) && !((i >> 16) & 1u))
+            throw std::runtime_error(std::string("[") + what + "] matrix " + std::to_string(b) + " of " +
+                                     std::to_string(batch) + " did not converge (" + std::to_string(i & 0xFFFFu) +
+                                     " iterations).");
+    }
+}
+
+}  // namespace
+
+// reference: src/eigh.mm:911-958 (core::eigh)
+void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
     require_gpu_allowed("eigh");
-    invalid("[eigh] not available in this build yet");
+    if (a.rows != a.cols) invalid("[eigh] Input matrices must be square.");
+    const uint32_t n = a.cols, B = a.batch;
+    if (B == 0) return;
+    if (n == 0) {
+        if (info) {
+            Call call;
+            uint32_t* di = call.out(info, B);
+            MLA_HIP(hipMemsetAsync(di, 0, (size_t)B * sizeof(uint32_t), call.stream()));
+            call.finish();
+        }
+        return;
+    }
+    if (!eigh_small_fits(n))
+        invalid("[eigh] n = " + std::to_string(n) + ": this build's eigh kernels take n <= 64 so far");
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    float* dw = call.out(w, (size_t)B * n);
+    float* dv = v ? call.out(v, (size_t)B * n * n) : nullptr;
+    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+    eigh_small(da, dw, dv, di, B, n, lower, call.stream());
+    check_converged(di, B, call.stream(), "eigh");
+    call.finish();
 }
 
 void svd(const Matrices&, float*, float*, float*, uint32_t*) {

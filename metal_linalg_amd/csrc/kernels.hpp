@@ -29,4 +29,9 @@ void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint
 void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
                 bool unit, hipStream_t s);
 
+// ---- symmetric eigendecomposition, n <= 64 ----
+bool eigh_small_fits(uint32_t n);
+void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
+                hipStream_t s);
+
 }  // namespace mla
