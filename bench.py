@@ -34,6 +34,15 @@ METRIC = "batched matrices/s (QR/eigh/SVD/chol/LU) + fp32 GFLOP/s & % peak at n=
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
 
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a 256 MiB copy kernel's readings (FETCH_SIZE
+# x1.9998, WRITE_SIZE x1.0); the runs and the scaling are in
+# profiles/<kernel>_<workload>.md.  Workloads not yet counted report null.
+TRAFFIC_BYTES = {
+    "eigh": 54_815_459 + 68_295_067,   # profiles/eigh_small_eigh.md
+    "qr": 42_169_219 + 81_920_000,     # profiles/qr_small_qr.md
+}
+
 
 class Workload:
     """name, inputs, the device call, and the accounting for one config."""
@@ -153,7 +162,7 @@ def main():
     if wl.bound == "hbm":
         achieved = wl.bytes_per_call / avg_kernel_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None}
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": TRAFFIC_BYTES.get(wl.name)}
     else:
         achieved = wl.flops_per_call / avg_kernel_s / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
