@@ -115,9 +115,33 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
     call.finish();
 }
 
-void svd(const Matrices&, float*, float*, float*, uint32_t*) {
+// reference: src/svd.mm:1058-1106 (core::svd)
+void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
     require_gpu_allowed("svd");
-    invalid("[svd] not available in this build yet");
+    const uint32_t M = a.rows, N = a.cols, K = std::min(M, N), B = a.batch;
+    if (B == 0) return;
+    if (K == 0) {
+        if (info) {
+            Call call;
+            uint32_t* di = call.out(info, B);
+            MLA_HIP(hipMemsetAsync(di, 0, (size_t)B * sizeof(uint32_t), call.stream()));
+            call.finish();
+        }
+        return;
+    }
+    if (!svd_small_fits(M, N))
+        invalid("[svd] " + std::to_string(M) + "x" + std::to_string(N) +
+                ": this build's SVD kernels take min(M, N) <= 64 and max(M, N) <= 128 so far");
+    Call call;
+    const float* da = call.in(a.data, (size_t)B * M * N);
+    float* ds = call.out(s, (size_t)B * K);
+    float* du = u ? call.out(u, (size_t)B * M * K) : nullptr;
+    float* dvt = vt ? call.out(vt, (size_t)B * K * N) : nullptr;
+    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+    float* ws = static_cast<float*>(call.scratch(svd_small_workspace(M, N, B)));
+    svd_small(da, du, ds, dvt, di, ws, B, M, N, call.stream());
+    check_converged(di, B, call.stream(), "svd");
+    call.finish();
 }
 
 namespace {

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 
 namespace mla {
@@ -33,5 +34,11 @@ void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32
 bool eigh_small_fits(uint32_t n);
 void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
                 hipStream_t s);
+
+// ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128 ----
+bool svd_small_fits(uint32_t m, uint32_t n);
+size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes
+void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, float* ws, uint32_t batch, uint32_t m,
+               uint32_t n, hipStream_t st);
 
 }  // namespace mla
