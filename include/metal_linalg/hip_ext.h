@@ -28,6 +28,16 @@ int metal_linalg_hip_kernel_time(const char* name, uint64_t* launches, double* t
 /* The names of the kernels timed since the last reset, one per line. */
 const char* metal_linalg_hip_kernel_names(void);
 
+/* The fp32 matrix-core GEMM the blocked factorisations use, on caller
+ * buffers (host or device): C = alpha op(A) op(B) + beta C, row-major;
+ * op(A) is A (M x K, stored with row stride lda) or, with transa, A^T (A
+ * stored K x M); likewise B (K x N) or, with transb, B stored N x K; `batch`
+ * products with element strides stride_a/b/c.  Returns a metal_linalg_status
+ * value.  For tests and measurement. */
+int metal_linalg_hip_sgemm(int transa, int transb, int M, int N, int K, float alpha, const float* A, int lda,
+                           long long stride_a, const float* B, int ldb, long long stride_b, float beta, float* C,
+                           int ldc, long long stride_c, int batch);
+
 /* The device's gcnArchName ("" without a GPU). */
 const char* metal_linalg_hip_arch(void);
 

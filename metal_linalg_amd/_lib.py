@@ -93,6 +93,9 @@ hip_kernel_time = _fn("metal_linalg_hip_kernel_time", _int, _cstr, ctypes.POINTE
                       ctypes.POINTER(ctypes.c_double))
 hip_kernel_names = _fn("metal_linalg_hip_kernel_names", _cstr)
 hip_arch = _fn("metal_linalg_hip_arch", _cstr)
+_ll = ctypes.c_longlong
+hip_sgemm = _fn("metal_linalg_hip_sgemm", _int, _int, _int, _int, _int, _int, ctypes.c_float, _p, _int, _ll, _p, _int,
+                _ll, ctypes.c_float, _p, _int, _ll, _int)
 
 
 def _struct(name, fields):

@@ -1,0 +1,254 @@
+// fp32 GEMM on the MI355X's matrix cores (v_mfma_f32_32x32x2f32), for the
+// trailing-matrix updates of the blocked factorisations:
+//
+//     C = alpha * op(A) * op(B) + beta * C,   all row-major, strided batches
+//
+// op(A) is A (M x K, lda) or A^T (A stored K x M); op(B) is B (K x N) or B^T
+// (B stored N x K).  Takes the place of the reference's MPS products
+// (reference: src/band_reduce.mm:159-174, src/cholesky_gpu.mm:184-198,
+// src/lu_gpu.mm:99-112).
+//
+// Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; each of its
+// four waves a 64 x 64 quarter as 2 x 2 blocks of 32 x 32 MFMA accumulators
+// (16 floats per lane each).  K advances 16 at a time through LDS, double
+// buffered: the next tile is loaded into registers while the current one
+// feeds the matrix cores.  Both operands sit in LDS k-contiguous ([row][k],
+// pitch 20 floats), and the K index of the 2-wide MFMA steps is permuted so
+// that a lane's eight k values for one tile are contiguous: lanes 0-31
+// supply k = 0..7 and lanes 32-63 k = 8..15 of the tile, read with two
+// conflict-free ds_read_b128.  (A permutation of the summation index applied
+// to both operands leaves the product unchanged.)
+#include <new>
+#include <stdexcept>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mla {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int LP = BK + 4;   // LDS pitch (floats): conflict-free b128 reads
+
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    int lda, ldb, ldc;
+    long long sa, sb, sc;   // batch strides (floats)
+    float alpha, beta;
+};
+
+// Loads this thread's share of a 128 x 16 operand tile (rows r0.., k0..) into
+// registers: 2048 floats = 256 threads x 8.  TRANS = the operand is stored
+// k-major (element (row, k) at p[k * ld + row]): op(A) = A^T, and op(B) = B
+// (whose tile rows are B's columns).
+template <bool TRANS>
+__device__ __forceinline__ void load_tile(const float* __restrict__ p, int ld, int rows, int K, int r0, int k0,
+                                          float (&reg)[8]) {
+    const int t = threadIdx.x;
+    if (!TRANS) {
+        // 4 consecutive threads cover 16 k of one row: 64 B contiguous
+        const int kq = (t & 3) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = r0 + (t >> 2) + h * 64;
+            const int k = k0 + kq;
+            if (r < rows && k + 3 < K && (((uintptr_t)(p + (size_t)r * ld + k)) & 15) == 0) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (size_t)r * ld + k);
+                reg[h * 4 + 0] = v[0];
+                reg[h * 4 + 1] = v[1];
+                reg[h * 4 + 2] = v[2];
+                reg[h * 4 + 3] = v[3];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    reg[h * 4 + i] = (r < rows && k + i < K) ? p[(size_t)r * ld + k + i] : 0.0f;
+            }
+        }
+    } else {
+        // stored [k][row]: a row of 128 floats per k; thread t takes rows
+        // (t & 31) * 4 .. +3 of k = t >> 5 and of k + 8
+        const int rq = (t & 31) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = k0 + (t >> 5) + h * 8;
+            const int r = r0 + rq;
+            if (k < K && r + 3 < rows && (((uintptr_t)(p + (size_t)k * ld + r)) & 15) == 0) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (size_t)k * ld + r);
+                reg[h * 4 + 0] = v[0];
+                reg[h * 4 + 1] = v[1];
+                reg[h * 4 + 2] = v[2];
+                reg[h * 4 + 3] = v[3];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    reg[h * 4 + i] = (k < K && r + i < rows) ? p[(size_t)k * ld + r + i] : 0.0f;
+            }
+        }
+    }
+}
+
+// Registers of load_tile into the LDS tile s[row][k].
+template <bool TRANS>
+__device__ __forceinline__ void store_tile(float (*s)[LP], const float (&reg)[8]) {
+    const int t = threadIdx.x;
+    if (!TRANS) {
+        const int kq = (t & 3) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = (t >> 2) + h * 64;
+            floatx4 v = {reg[h * 4 + 0], reg[h * 4 + 1], reg[h * 4 + 2], reg[h * 4 + 3]};
+            *reinterpret_cast<floatx4*>(&s[r][kq]) = v;
+        }
+    } else {
+        const int rq = (t & 31) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = (t >> 5) + h * 8;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[rq + i][k] = reg[h * 4 + i];
+        }
+    }
+}
+
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+    __shared__ float As[2][BM][LP];
+    __shared__ float Bs[2][BN][LP];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const size_t bz = blockIdx.z;
+    const float* A = g.A + bz * g.sa;
+    const float* B = g.B + bz * g.sb;
+    float* C = g.C + bz * g.sc;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    float ra[8], rb[8];
+    load_tile<TA>(A, g.lda, g.M, g.K, m0, 0, ra);
+    load_tile<!TB>(B, g.ldb, g.N, g.K, n0, 0, rb);
+    store_tile<TA>(As[0], ra);
+    store_tile<!TB>(Bs[0], rb);
+    __syncthreads();
+
+    const int ktiles = (g.K + BK - 1) / BK;
+    const int lr = lane & 31;         // row (A) / column (B) within a 32-block
+    const int kh = (lane >> 5) * 8;   // this lane's 8 k values of the tile
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < ktiles) {
+            load_tile<TA>(A, g.lda, g.M, g.K, m0, (kt + 1) * BK, ra);
+            load_tile<!TB>(B, g.ldb, g.N, g.K, n0, (kt + 1) * BK, rb);
+        }
+        floatx4 a0[2][2], b0[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            a0[i][0] = *reinterpret_cast<const floatx4*>(&As[cur][wm + i * 32 + lr][kh]);
+            a0[i][1] = *reinterpret_cast<const floatx4*>(&As[cur][wm + i * 32 + lr][kh + 4]);
+            b0[i][0] = *reinterpret_cast<const floatx4*>(&Bs[cur][wn + i * 32 + lr][kh]);
+            b0[i][1] = *reinterpret_cast<const floatx4*>(&Bs[cur][wn + i * 32 + lr][kh + 4]);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i][s >> 2][s & 3], b0[j][s >> 2][s & 3],
+                                                                     acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < ktiles) {
+            store_tile<TA>(As[cur ^ 1], ra);
+            store_tile<!TB>(Bs[cur ^ 1], rb);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: lane holds column (lane & 31) of each 32 x 32 block, rows
+    // 8 * (e / 4) + 4 * (lane / 32) + (e % 4)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn + j * 32 + lr;
+            if (col >= g.N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row < g.M) {
+                    float* cp = C + (size_t)row * g.ldc + col;
+                    const float v = g.alpha * acc[i][j][e];
+                    *cp = g.beta == 0.0f ? v : fmaf(g.beta, *cp, v);
+                }
+            }
+        }
+}
+
+}  // namespace
+
+void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
+           const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
+           hipStream_t s) {
+    if (M <= 0 || N <= 0 || batch <= 0) return;
+    GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta};
+    const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
+    KernelTimer t("gemm_mfma", s);
+    if (!ta && !tb) hipLaunchKernelGGL((gemm_kernel<false, false>), grid, dim3(256), 0, s, g);
+    else if (!ta && tb) hipLaunchKernelGGL((gemm_kernel<false, true>), grid, dim3(256), 0, s, g);
+    else if (ta && !tb) hipLaunchKernelGGL((gemm_kernel<true, false>), grid, dim3(256), 0, s, g);
+    else hipLaunchKernelGGL((gemm_kernel<true, true>), grid, dim3(256), 0, s, g);
+    t.stop();
+    MLA_HIP(hipGetLastError());
+}
+
+}  // namespace mla
+
+// Test and measurement hook (include/metal_linalg/hip_ext.h): the MFMA GEMM
+// on caller buffers (host or device), row-major, strided batches.
+extern "C" int metal_linalg_hip_sgemm(int transa, int transb, int M, int N, int K, float alpha, const float* A,
+                                      int lda, long long stride_a, const float* B, int ldb, long long stride_b,
+                                      float beta, float* C, int ldc, long long stride_c, int batch) {
+    try {
+        if (M < 0 || N < 0 || K < 0 || batch < 0) return 1;
+        if (!M || !N || !batch) return 0;
+        mla::Call call;
+        const long long ra = transa ? K : M, ca = transa ? M : K;
+        const long long rb = transb ? N : K, cb = transb ? K : N;
+        const size_t na = (size_t)((batch - 1) * stride_a + (ra - 1) * lda + ca);
+        const size_t nb = (size_t)((batch - 1) * stride_b + (rb - 1) * ldb + cb);
+        const size_t nc = (size_t)((batch - 1) * stride_c + (long long)(M - 1) * ldc + N);
+        const float* dA = K ? call.in(A, na) : nullptr;
+        const float* dB = K ? call.in(B, nb) : nullptr;
+        float* dC = call.out(C, nc);
+        if (beta != 0.0f) {
+            // C is also an input: a host C must be copied in first
+            const float* cin = call.in(C, nc);
+            if (cin != dC) MLA_HIP(hipMemcpyAsync(dC, cin, nc * sizeof(float), hipMemcpyDeviceToDevice, call.stream()));
+        }
+        mla::sgemm(transa != 0, transb != 0, M, N, K, alpha, dA, lda, stride_a, dB, ldb, stride_b, beta, dC, ldc,
+                   stride_c, batch, call.stream());
+        call.finish();
+        return 0;
+    } catch (const std::invalid_argument&) {
+        return 1;
+    } catch (const std::bad_alloc&) {
+        return 3;
+    } catch (...) {
+        return 2;
+    }
+}

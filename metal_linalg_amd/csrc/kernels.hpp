@@ -41,4 +41,9 @@ size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes
 void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, float* ws, uint32_t batch, uint32_t m,
                uint32_t n, hipStream_t st);
 
+// ---- fp32 MFMA GEMM: C = alpha op(A) op(B) + beta C, row-major, strided batches ----
+void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
+           const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
+           hipStream_t s);
+
 }  // namespace mla
