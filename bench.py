@@ -45,14 +45,37 @@ TRAFFIC_BYTES = {
 
 
 class Workload:
-    """name, inputs, the device call, and the accounting for one config."""
+    """name, inputs, the device call, and the accounting for one config.
+
+    bytes_per_call / flops_per_call are the algorithmic HBM bytes / flops of
+    the roofline kernel(s) per call.  `unit` is "matrices/s" for the batched
+    configs and "GFLOP/s" for the single large matrix, where `nominal_flops`
+    (the textbook count of the whole decomposition) per call is the numerator.
+    """
 
     def __init__(self, name, desc, batch, make, call, kernel, bytes_per_call, flops_per_call, bound, oracle_call,
-                 shape):
+                 shape, unit="matrices/s", nominal_flops=None):
         self.name, self.desc, self.batch = name, desc, batch
         self.make, self.call, self.kernel = make, call, kernel
         self.bytes_per_call, self.flops_per_call, self.bound = bytes_per_call, flops_per_call, bound
         self.oracle_call, self.shape = oracle_call, shape
+        self.unit, self.nominal_flops = unit, nominal_flops
+
+    def rate(self, calls, seconds):
+        if self.unit == "GFLOP/s":
+            return self.nominal_flops * calls / seconds / 1e9
+        return self.batch * calls / seconds
+
+
+def blocked_chol_gemm_flops(n, nb=128):
+    """Flops of the blocked Cholesky's matrix-core updates: per panel, the
+    TRSM as a product (2 m2 nb^2) and the lower half of the SYRK (m2^2 nb)."""
+    f = 0
+    for j in range(0, n, nb):
+        b = min(nb, n - j)
+        m2 = n - j - b
+        f += 2 * m2 * b * b + m2 * m2 * b
+    return f
 
 
 def workloads():
@@ -118,6 +141,16 @@ def workloads():
         lu_make, lambda api, t: api.solve_triangular(t["a"], t["b"], False, True), "trsm_small",
         8192 * (1024 + 256 + 256), 8192 * 1024, "hbm",
         lambda o, h, n: o.solve_triangular(h["a"][:n], h["b"][:n], False, True), {"batch": 8192, "n": 16, "nrhs": 4})
+
+    def chol5_make():
+        return {"a": U.config5_spd(U.config5_matrix())}
+
+    n5 = 4096
+    w["cholesky4096"] = Workload(
+        "cholesky4096", "cholesky lower, one 4096x4096 SPD fp32 G G^T/n + I, G ~ N(0,1) (BASELINE config 5)", 1,
+        chol5_make, lambda api, t: api.cholesky(t["a"], False), "gemm_mfma", None,
+        blocked_chol_gemm_flops(n5), "mfma", lambda o, h, n: o.cholesky(h["a"][None], False), {"n": n5},
+        unit="GFLOP/s", nominal_flops=n5 ** 3 / 3)
     return w
 
 
@@ -166,24 +199,28 @@ def main():
     # the path's kernels (one name, or several launched once per call each)
     names = wl.kernel if isinstance(wl.kernel, (list, tuple)) else [wl.kernel]
     per = [_lib.kernel_time(k) for k in names]
-    launches = min(p[0] for p in per)
+    launches = sum(p[0] for p in per)
     kernel_ms = sum(p[1] for p in per)
     other = {n: _lib.kernel_time(n) for n in _lib.kernel_names()}
+    # per call: the roofline kernels' summed HIP-event time over the timed steps
+    kernel_s_per_call = (kernel_ms / 1e3) / args.steps
     avg_kernel_s = (kernel_ms / 1e3) / max(launches, 1)
     ms_per_step = elapsed * 1e3 / args.steps
-    value = wl.batch * args.steps / elapsed
+    value = wl.rate(args.steps, elapsed)
 
     if wl.bound == "hbm":
-        achieved = wl.bytes_per_call / avg_kernel_s / 1e9
+        achieved = wl.bytes_per_call / kernel_s_per_call / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": TRAFFIC_BYTES.get(wl.name)}
     else:
-        achieved = wl.flops_per_call / avg_kernel_s / 1e12
+        achieved = wl.flops_per_call / kernel_s_per_call / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_MFMA_PEAK_TFS, 5), "traffic": None}
     roof["kernel"] = "+".join(names)
     roof["kernel_avg_us"] = round(avg_kernel_s * 1e6, 3)
     roof["launches"] = launches
+    roof["launches_per_call"] = launches / args.steps
+    roof["kernel_us_per_call"] = round(kernel_s_per_call * 1e6, 3)
     roof["algorithmic_bytes_per_launch"] = wl.bytes_per_call
     roof["algorithmic_flops_per_launch"] = wl.flops_per_call
 
@@ -192,7 +229,7 @@ def main():
     reps = max(1, min(5, args.steps))
     for _ in range(reps):
         wl.call(api, host)
-    host_rate = wl.batch * reps / (time.perf_counter() - t0)
+    host_rate = wl.rate(reps, time.perf_counter() - t0)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -209,14 +246,14 @@ def main():
             if time.perf_counter() - t0 >= args.cpu_seconds:
                 break
         cpu_s = time.perf_counter() - t0
-        cpu = {"value": round(count / cpu_s, 2), "unit": "matrices/s", "cores": oracle.threads(), "kind": "port",
+        cpu = {"value": round(wl.rate(count / wl.batch, cpu_s), 2), "unit": wl.unit, "cores": oracle.threads(), "kind": "port",
                "sample": f"{count} matrices ({count // n} passes over the full {wl.batch}-matrix batch) in "
                          f"{cpu_s:.2f} s wall on {oracle.threads()} threads; {oracle.config()}"}
 
     line = {
         "metric": METRIC,
         "value": round(value, 2),
-        "unit": "matrices/s",
+        "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,

@@ -165,12 +165,17 @@ void cholesky(const Matrices& a, bool upper, float* l, uint32_t* info) {
     require_square(a, "cholesky");
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0) return;
-    if (!chol_small_fits(n)) too_large("cholesky", n);
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dl = call.out(l, (size_t)B * n * n);
-    uint32_t* di = call.out(info, B);
-    chol_small(da, dl, di, B, n, upper, call.stream());
+    if (chol_small_fits(n)) {
+        uint32_t* di = call.out(info, B);
+        chol_small(da, dl, di, B, n, upper, call.stream());
+    } else {
+        uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+        float* work = static_cast<float*>(call.scratch(chol_blocked_workspace(n)));
+        chol_blocked(da, dl, di, work, work + (size_t)n * n, B, n, upper, call.stream());
+    }
     call.finish();
 }
 

@@ -42,6 +42,7 @@ struct GemmArgs {
     int lda, ldb, ldc;
     long long sa, sb, sc;   // batch strides (floats)
     float alpha, beta;
+    int lower;   // 1: only tiles that reach the lower triangle (row >= col) of C
 };
 
 // Loads this thread's share of a 128 x 16 operand tile (rows r0.., k0..) into
@@ -126,6 +127,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const int wave = t >> 6;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    if (g.lower && n0 >= m0 + BM) return;   // tile strictly above the diagonal (uniform)
     const size_t bz = blockIdx.z;
     const float* A = g.A + bz * g.sa;
     const float* B = g.B + bz * g.sb;
@@ -203,9 +205,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
            const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
-           hipStream_t s) {
+           hipStream_t s, bool lower_only) {
     if (M <= 0 || N <= 0 || batch <= 0) return;
-    GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta};
+    GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta, lower_only ? 1 : 0};
     const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
     KernelTimer t("gemm_mfma", s);
     if (!ta && !tb) hipLaunchKernelGGL((gemm_kernel<false, false>), grid, dim3(256), 0, s, g);

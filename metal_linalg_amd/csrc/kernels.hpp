@@ -20,6 +20,13 @@ void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, ui
 bool chol_small_fits(uint32_t n);
 void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s);
 
+// Blocked Cholesky, any n, one matrix at a time: work = chol_blocked_workspace(n)
+// bytes (n x n working copy + the 128 x 128 triangular inverse).  `info` must
+// be device memory (never NULL).
+size_t chol_blocked_workspace(uint32_t n);
+void chol_blocked(const float* a, float* l, uint32_t* info, float* work, float* xinv, uint32_t batch, uint32_t n,
+                  bool upper, hipStream_t s);
+
 // ---- LU, solve, inverse, triangular solve, n <= 32 ----
 bool lu_small_fits(uint32_t n);
 void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
@@ -44,6 +51,6 @@ void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, fl
 // ---- fp32 MFMA GEMM: C = alpha op(A) op(B) + beta C, row-major, strided batches ----
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
            const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
-           hipStream_t s);
+           hipStream_t s, bool lower_only = false);
 
 }  // namespace mla

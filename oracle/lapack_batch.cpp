@@ -129,7 +129,16 @@ template <class F>
 void lapack_batches(uint32_t batch, const F& f) {
     const uint32_t threads = std::min<uint32_t>(thread_count(), batch);
     if (threads <= 1) {
-        f(0u, batch);
+        // one matrix (or one thread): LAPACK's own threads, as the reference
+        // leaves Accelerate threaded there (metal_runtime.mm:413-416)
+        if (g_lapack.set_num_threads) g_lapack.set_num_threads((int)thread_count());
+        try {
+            f(0u, batch);
+        } catch (...) {
+            if (g_lapack.set_num_threads) g_lapack.set_num_threads(1);
+            throw;
+        }
+        if (g_lapack.set_num_threads) g_lapack.set_num_threads(1);
         return;
     }
     const uint32_t chunks = std::min<uint32_t>(batch, threads * 4);   // kChunksPerThread

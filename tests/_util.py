@@ -167,3 +167,15 @@ def lu_residual(a, lu, piv):
     perm, L, U = lu_unpack(lu, piv)
     pa = np.take_along_axis(a.astype(np.float64), perm[..., :, None], axis=-2)
     return rel_recon(pa, L @ U)
+
+
+def config5_matrix(n=4096, seed=6):
+    """G, iid N(0,1), the single large matrix of config 5."""
+    return gaussian((n, n), seed)
+
+
+def config5_spd(g):
+    """G G^T / n + I, in float64, rounded to float32."""
+    n = g.shape[0]
+    g64 = g.astype(np.float64)
+    return (g64 @ g64.T / n + np.eye(n)).astype(np.float32)
