@@ -52,52 +52,114 @@ __global__ __launch_bounds__(256) void copy_transpose_kernel(const float* __rest
     }
 }
 
+// One workgroup factors the nb x nb diagonal block (nb <= 128, padded to 128
+// with the identity) and forms the inverse X = L^-1 of its factor in the same
+// sweep.  Thread t owns the 8 x 8 blocks at block row bi = t >> 4 and block
+// column bj = t & 15 of both A (a[i][j] = A[8 bi + i][8 bj + j]) and X.
+//
+// Step k: the threads of block column k / 8 publish their A blocks to LDS
+// transposed (so column k is contiguous), the threads of block row k / 8
+// their X blocks (so row k is contiguous).  With d = A[k][k],
+// inv = 1 / sqrt(d) and g = inv^2, every thread then applies
+//   a[i][j] -= A[r][k] * lc(c),      x[i][j] -= lc(r) * X[k][c],
+//   lc(q) = A[q][k] g (q > k),  1 - inv (q = k),  0 (q < k)
+// (r = 8 bi + i, c = 8 bj + j; A[r][k] taken as 0 for r < k).  For the
+// columns right of k this is the right-looking update
+// A[r][c] -= L[r][k] L[c][k]; on column k it scales to L[r][k] = A[r][k] inv;
+// on X it scales row k by inv and performs the forward substitution
+// X[r] -= L[r][k] X[k] for the rows below.  Entries above the diagonal of A
+// pick up one finite value each (row k, from A[k][k]) that is never read
+// again: the output takes the lower triangle, the diagonal from the saved
+// pivots.  X stays exactly lower triangular.  The published blocks alternate between two LDS slots, so one
+// barrier per step suffices: a slot is rewritten two steps later, after
+// every thread has passed the barrier that follows its reads.
+//
+// The first pivot that is not positive and finite sets info = j0 + k + 1
+// (unless an earlier block already set it); the block carries on with NaN,
+// which the final extract turns into the all-NaN output.
+struct DiagSlot {
+    float a[8][NB];   // a[j][r] = A[r][8 kb + j]: block column kb, transposed
+    float x[8][NB];   // x[i][c] = X[8 kb + i][c]: block row kb
+};
+
 __global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ W, int ld, int j0, int nb,
                                                         float* __restrict__ X, uint32_t* __restrict__ info) {
-    __shared__ float L[NB][NB + 1];
-    __shared__ float Xs[NB][NB + 1];
-    __shared__ int fail;
+    __shared__ DiagSlot slot[2];
+    __shared__ float piv[NB];
     const int t = threadIdx.x;
-    for (int idx = t; idx < nb * nb; idx += 256) {
-        const int r = idx / nb, c = idx - r * nb;
-        L[r][c] = c <= r ? W[(size_t)(j0 + r) * ld + j0 + c] : 0.0f;
-        Xs[r][c] = r == c ? 1.0f : 0.0f;
-    }
-    if (t == 0) fail = 0;
-    __syncthreads();
-    for (int k = 0; k < nb; ++k) {
-        if (t == 0) {
-            const float d = L[k][k];
-            if (!(d > 0.0f && d <= FLT_MAX) && fail == 0) fail = k + 1;
-            L[k][k] = sqrtf(d);
+    const int bi = t >> 4, bj = t & 15;
+    const int r0 = 8 * bi, c0 = 8 * bj;
+    float a[8][8], x[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int r = r0 + i, c = c0 + j;
+            a[i][j] = (r < nb && c < nb) ? (c <= r ? W[(size_t)(j0 + r) * ld + j0 + c] : 0.0f)
+                                         : (r == c ? 1.0f : 0.0f);
+            x[i][j] = r == c ? 1.0f : 0.0f;
+        }
+    int fail = 0;
+    for (int k = 0; k < NB; ++k) {
+        DiagSlot& S = slot[k & 1];
+        const int kb = k >> 3, kk = k & 7;
+        if (bj == kb) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                *reinterpret_cast<float4*>(&S.a[j][r0]) = make_float4(a[0][j], a[1][j], a[2][j], a[3][j]);
+                *reinterpret_cast<float4*>(&S.a[j][r0 + 4]) = make_float4(a[4][j], a[5][j], a[6][j], a[7][j]);
+            }
+        }
+        if (bi == kb) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                *reinterpret_cast<float4*>(&S.x[i][c0]) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
+                *reinterpret_cast<float4*>(&S.x[i][c0 + 4]) = make_float4(x[i][4], x[i][5], x[i][6], x[i][7]);
+            }
         }
         __syncthreads();
-        const float inv = 1.0f / L[k][k];
-        for (int r = k + 1 + t; r < nb; r += 256) L[r][k] *= inv;
-        __syncthreads();
-        const int w = nb - k - 1;
-        for (int p = t; p < w * w; p += 256) {
-            const int r = k + 1 + p / w, c = k + 1 + p % w;
-            if (c <= r) L[r][c] = fmaf(-L[r][k], L[c][k], L[r][c]);
+        const float* colk = S.a[kk];   // column k of A
+        const float* rowk = S.x[kk];   // row k of X
+        const float d = colk[k];
+        if (fail == 0 && !(d > 0.0f && d <= FLT_MAX)) fail = k + 1;
+        const float p = sqrtf(d);
+        const float inv = 1.0f / p;
+        const float g = inv * inv, one = 1.0f - inv;
+        if (t == 0) piv[k] = p;
+        const float4 cr0 = *reinterpret_cast<const float4*>(&colk[r0]);
+        const float4 cr1 = *reinterpret_cast<const float4*>(&colk[r0 + 4]);
+        const float4 cc0 = *reinterpret_cast<const float4*>(&colk[c0]);
+        const float4 cc1 = *reinterpret_cast<const float4*>(&colk[c0 + 4]);
+        const float4 xr0 = *reinterpret_cast<const float4*>(&rowk[c0]);
+        const float4 xr1 = *reinterpret_cast<const float4*>(&rowk[c0 + 4]);
+        float cr[8] = {cr0.x, cr0.y, cr0.z, cr0.w, cr1.x, cr1.y, cr1.z, cr1.w};
+        const float cc[8] = {cc0.x, cc0.y, cc0.z, cc0.w, cc1.x, cc1.y, cc1.z, cc1.w};
+        const float xk[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
+        float lr[8], lcol[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            lr[q] = r0 + q > k ? cr[q] * g : (r0 + q == k ? one : 0.0f);
+            lcol[q] = c0 + q > k ? cc[q] * g : (c0 + q == k ? one : 0.0f);
+            cr[q] = r0 + q < k ? 0.0f : cr[q];   // above the diagonal: not an entry of L
         }
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                a[i][j] = fmaf(-cr[i], lcol[j], a[i][j]);
+                x[i][j] = fmaf(-lr[i], xk[j], x[i][j]);
+            }
     }
-    // X = L^-1: forward substitution on the identity, row k then the rows below
-    for (int k = 0; k < nb; ++k) {
-        const float inv = 1.0f / L[k][k];
-        for (int c = t; c <= k; c += 256) Xs[k][c] *= inv;
-        __syncthreads();
-        const int w = nb - k - 1, h = k + 1;
-        for (int p = t; p < w * h; p += 256) {
-            const int i = k + 1 + p / h, c = p % h;
-            Xs[i][c] = fmaf(-L[i][k], Xs[k][c], Xs[i][c]);
+    __syncthreads();   // piv complete
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = r0 + i;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = c0 + j;
+            if (r < nb && c <= r) W[(size_t)(j0 + r) * ld + j0 + c] = r == c ? piv[r] : a[i][j];
+            if (r < nb && c < nb) X[(size_t)r * nb + c] = x[i][j];
         }
-        __syncthreads();
-    }
-    for (int idx = t; idx < nb * nb; idx += 256) {
-        const int r = idx / nb, c = idx - r * nb;
-        if (c <= r) W[(size_t)(j0 + r) * ld + j0 + c] = L[r][c];
-        X[(size_t)r * nb + c] = Xs[r][c];
     }
     if (t == 0 && fail != 0 && *info == 0) *info = (uint32_t)(j0 + fail);
 }
