@@ -67,6 +67,21 @@ class Workload:
         return self.batch * calls / seconds
 
 
+def blocked_lu_gemm_flops(n, nb=128, w=16):
+    """Flops of the blocked LU's matrix-core updates: inside each panel the
+    leaf updates (rows below the leaf x the panel's later columns x w), and
+    per panel the trailing A22 -= L21 U12."""
+    f = 0
+    for pj in range(0, n, nb):
+        pe = min(pj + nb, n)
+        for pc in range(pj, pe, w):
+            ww = min(w, pe - pc)
+            f += 2 * (n - pc - ww) * (pe - pc - ww) * ww
+        nc = n - pe
+        f += 2 * nc * nc * (pe - pj)
+    return f
+
+
 def blocked_chol_gemm_flops(n, nb=128):
     """Flops of the blocked Cholesky's matrix-core updates: per panel, the
     TRSM as a product (2 m2 nb^2) and the lower half of the SYRK (m2^2 nb)."""
@@ -151,6 +166,14 @@ def workloads():
         chol5_make, lambda api, t: api.cholesky(t["a"], False), "gemm_mfma", None,
         blocked_chol_gemm_flops(n5), "mfma", lambda o, h, n: o.cholesky(h["a"][None], False), {"n": n5},
         unit="GFLOP/s", nominal_flops=n5 ** 3 / 3)
+
+    def lu5_make():
+        return {"a": U.config5_matrix()}
+
+    w["lu4096"] = Workload(
+        "lu4096", "lu_factor, one 4096x4096 fp32 G ~ N(0,1) (BASELINE config 5)", 1, lu5_make,
+        lambda api, t: api.lu_factor(t["a"]), "gemm_mfma", None, blocked_lu_gemm_flops(n5), "mfma",
+        lambda o, h, n: o.lu_factor(h["a"][None]), {"n": n5}, unit="GFLOP/s", nominal_flops=2 * n5 ** 3 / 3)
     return w
 
 

@@ -152,9 +152,9 @@ void require_square(const Matrices& a, const char* what) {
                 std::to_string(a.cols) + ".");
 }
 
-[[noreturn]] void too_large(const char* what, uint32_t n) {
-    invalid(std::string("[") + what + "] n = " + std::to_string(n) +
-            ": this build's kernels for this decomposition take n <= 32 so far");
+[[noreturn]] void too_large(const char* what, uint32_t n, uint32_t limit) {
+    invalid(std::string("[") + what + "] n = " + std::to_string(n) + ": this build's kernels take n <= " +
+            std::to_string(limit));
 }
 
 }  // namespace
@@ -185,13 +185,18 @@ void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
     require_square(a, "lu_factor");
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0) return;
-    if (!lu_small_fits(n)) too_large("lu_factor", n);
+    if (!lu_blocked_fits(n)) too_large("lu_factor", n, 16384);
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dlu = call.out(lu, (size_t)B * n * n);
     uint32_t* dp = call.out(pivots, (size_t)B * n);
-    uint32_t* di = call.out(info, B);
-    lu_small_factor(da, dlu, dp, di, B, n, call.stream());
+    if (lu_small_fits(n)) {
+        uint32_t* di = call.out(info, B);
+        lu_small_factor(da, dlu, dp, di, B, n, call.stream());
+    } else {
+        uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+        lu_blocked_factor(da, dlu, dp, di, B, n, call.stream());
+    }
     call.finish();
 }
 
@@ -208,13 +213,19 @@ void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t*
         }
         return;
     }
-    if (!lu_small_fits(n)) too_large("solve", n);
+    if (!lu_blocked_fits(n)) too_large("solve", n, 16384);
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    uint32_t* di = call.out(info, B);
-    lu_small_solve(da, db, nrhs, dx, di, B, n, call.stream());
+    if (lu_small_fits(n)) {
+        uint32_t* di = call.out(info, B);
+        lu_small_solve(da, db, nrhs, dx, di, B, n, call.stream());
+    } else {
+        uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+        float* work = static_cast<float*>(call.scratch(lu_blocked_workspace(n)));
+        lu_blocked_solve(da, db, nrhs, dx, di, work, B, n, call.stream());
+    }
     call.finish();
 }
 
@@ -223,12 +234,18 @@ void inv(const Matrices& a, float* x, uint32_t* info) {
     require_square(a, "inv");
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0) return;
-    if (!lu_small_fits(n)) too_large("inv", n);
+    if (!lu_blocked_fits(n)) too_large("inv", n, 16384);
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dx = call.out(x, (size_t)B * n * n);
-    uint32_t* di = call.out(info, B);
-    lu_small_inv(da, dx, di, B, n, call.stream());
+    if (lu_small_fits(n)) {
+        uint32_t* di = call.out(info, B);
+        lu_small_inv(da, dx, di, B, n, call.stream());
+    } else {
+        uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+        float* work = static_cast<float*>(call.scratch(lu_blocked_workspace(n)));
+        lu_blocked_solve(da, nullptr, n, dx, di, work, B, n, call.stream());
+    }
     call.finish();
 }
 
@@ -238,12 +255,20 @@ void solve_triangular(const Matrices& a, const float* b, uint32_t nrhs, bool upp
     require_square(a, "solve_triangular");
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0 || nrhs == 0) return;
-    if (!lu_small_fits(n)) too_large("solve_triangular", n);
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    trsm_small(da, db, dx, B, n, nrhs, upper, unit, call.stream());
+    if (lu_small_fits(n)) {
+        trsm_small(da, db, dx, B, n, nrhs, upper, unit, call.stream());
+    } else {
+        if (dx != db)
+            MLA_HIP(hipMemcpyAsync(dx, db, (size_t)B * n * nrhs * sizeof(float), hipMemcpyDeviceToDevice,
+                                   call.stream()));
+        for (uint32_t i = 0; i < B; ++i)
+            trsm_blocked_one(da + (size_t)i * n * n, (int)n, dx + (size_t)i * n * nrhs, (int)n, (int)nrhs, upper,
+                             unit, call.stream());
+    }
     call.finish();
 }
 

@@ -37,6 +37,18 @@ void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint
 void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
                 bool unit, hipStream_t s);
 
+// ---- LU and triangular solves for larger n (<= 16384), one matrix at a time ----
+// `info` must be device memory (never NULL); work = lu_blocked_workspace(n) bytes.
+bool lu_blocked_fits(uint32_t n);
+size_t lu_blocked_workspace(uint32_t n);
+void lu_blocked_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
+                       hipStream_t s);
+// X = A^-1 B (b == nullptr: X = A^-1), all NaN where info > 0
+void lu_blocked_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, float* work,
+                      uint32_t batch, uint32_t n, hipStream_t s);
+// B := T^-1 B in place for one n x n triangle T (row stride ldt), B n x nrhs
+void trsm_blocked_one(const float* T, int ldt, float* B, int n, int nrhs, bool upper, bool unit, hipStream_t s);
+
 // ---- symmetric eigendecomposition, n <= 64 ----
 bool eigh_small_fits(uint32_t n);
 void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
