@@ -195,7 +195,8 @@ void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
         lu_small_factor(da, dlu, dp, di, B, n, call.stream());
     } else {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
-        lu_blocked_factor(da, dlu, dp, di, B, n, call.stream());
+        float* work = static_cast<float*>(call.scratch(lu_panel_workspace(n)));
+        lu_blocked_factor(da, dlu, dp, di, work, B, n, call.stream());
     }
     call.finish();
 }

@@ -40,9 +40,10 @@ void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32
 // ---- LU and triangular solves for larger n (<= 16384), one matrix at a time ----
 // `info` must be device memory (never NULL); work = lu_blocked_workspace(n) bytes.
 bool lu_blocked_fits(uint32_t n);
-size_t lu_blocked_workspace(uint32_t n);
-void lu_blocked_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
-                       hipStream_t s);
+size_t lu_blocked_workspace(uint32_t n);   // solve / inv
+size_t lu_panel_workspace(uint32_t n);     // lu_factor
+void lu_blocked_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, float* work, uint32_t batch,
+                       uint32_t n, hipStream_t s);
 // X = A^-1 B (b == nullptr: X = A^-1), all NaN where info > 0
 void lu_blocked_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, float* work,
                       uint32_t batch, uint32_t n, hipStream_t s);
