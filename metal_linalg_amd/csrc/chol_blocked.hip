@@ -95,8 +95,11 @@ __global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ W, i
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int r = r0 + i, c = c0 + j;
-            a[i][j] = (r < nb && c < nb) ? (c <= r ? W[(size_t)(j0 + r) * ld + j0 + c] : 0.0f)
-                                         : (r == c ? 1.0f : 0.0f);
+            // unconditional load from a clamped address, then masked: all 64
+            // loads are in flight before the first wait
+            const bool in = r < nb && c < nb && c <= r;
+            const float v = W[in ? (size_t)(j0 + r) * ld + j0 + c : (size_t)j0 * ld + j0];
+            a[i][j] = in ? v : (r == c && (r >= nb || c >= nb) ? 1.0f : 0.0f);
             x[i][j] = r == c ? 1.0f : 0.0f;
         }
     int fail = 0;
