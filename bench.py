@@ -174,6 +174,24 @@ def workloads():
         "lu4096", "lu_factor, one 4096x4096 fp32 G ~ N(0,1) (BASELINE config 5)", 1, lu5_make,
         lambda api, t: api.lu_factor(t["a"]), "gemm_mfma", None, blocked_lu_gemm_flops(n5), "mfma",
         lambda o, h, n: o.lu_factor(h["a"][None]), {"n": n5}, unit="GFLOP/s", nominal_flops=2 * n5 ** 3 / 3)
+
+    def qr5_make():
+        return {"a": U.config5_matrix()}
+
+    def qr_gemm_flops(n, nb=128):
+        # the trailing updates and the formation of Q as products:
+        # per panel W = V^T A2, A2 -= V W, and the same for Q2
+        f = 0
+        for pj in range(0, n, nb):
+            pe = min(pj + nb, n)
+            b, rows, n2, nq = pe - pj, n - pj, n - pe, n - pj
+            f += 4 * rows * b * n2 + 4 * rows * b * nq
+        return f
+
+    w["qr4096"] = Workload(
+        "qr4096", "qr_with_mode reduced, one 4096x4096 fp32 G ~ N(0,1) (BASELINE config 5)", 1, qr5_make,
+        lambda api, t: api.qr(t["a"], "reduced"), "gemm_mfma", None, qr_gemm_flops(n5), "mfma",
+        lambda o, h, n: o.qr(h["a"][None], "reduced"), {"n": n5}, unit="GFLOP/s", nominal_flops=8 * n5 ** 3 / 3)
     return w
 
 

@@ -57,14 +57,20 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
         return;
     }
     if (K == 0 || B == 0) return;
-    if (!qr_small_fits(M, N, QC))
+    const bool small = qr_small_fits(M, N, QC);
+    if (!small && !qr_blocked_fits(M, N))
         invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) +
-                ": this build's QR kernels take at most 64 rows and 64 columns so far");
+                ": this build's QR kernels take at most 4096 rows so far");
     Call call;
     const float* da = call.in(a.data, (size_t)B * M * N);
     float* dq = QC ? call.out(q, (size_t)B * M * QC) : nullptr;
     float* dr = call.out(r, (size_t)B * RR * N);
-    qr_small(da, dq, dr, B, M, N, QC, RR, call.stream());
+    if (small) {
+        qr_small(da, dq, dr, B, M, N, QC, RR, call.stream());
+    } else {
+        float* work = static_cast<float*>(call.scratch(qr_blocked_workspace(M, N)));
+        qr_blocked(da, dq, dr, B, M, N, QC, RR, work, call.stream());
+    }
     call.finish();
 }
 

@@ -16,6 +16,13 @@ bool qr_small_fits(uint32_t m, uint32_t n, uint32_t qc);
 void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
               hipStream_t s);
 
+// ---- QR for larger matrices (m <= 4096), one matrix at a time ----
+// work = qr_blocked_workspace(m, n) bytes; q may be NULL when qc = 0.
+bool qr_blocked_fits(uint32_t m, uint32_t n);
+size_t qr_blocked_workspace(uint32_t m, uint32_t n);
+void qr_blocked(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
+                float* work, hipStream_t s);
+
 // ---- Cholesky, n <= 32 ----
 bool chol_small_fits(uint32_t n);
 void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s);

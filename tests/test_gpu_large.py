@@ -183,3 +183,80 @@ def test_config5_lu(cuda, api, oracle):
     # within a small factor of LAPACK's own.
     assert r <= bound(4096) and r <= 4 * ro + 1e-6
     assert int(io[0]) == 0
+
+
+# ---- QR (beyond 64 rows or columns: the blocked path) ----
+
+def _qr_check(a, q, r, ro, n_bound):
+    from _util import orthogonality, rel_recon
+
+    a64 = a.astype(np.float64)
+    r64 = r.astype(np.float64)
+    recon = ortho = None
+    if q is not None:
+        q64 = q.astype(np.float64)
+        recon, ortho = rel_recon(a64, q64 @ r64), orthogonality(q64)
+    # R is unique up to the signs of its rows: compare magnitudes with LAPACK's
+    scale = np.abs(ro).max(axis=(-2, -1), keepdims=True)
+    dr = (np.abs(np.abs(r64) - np.abs(ro)) / scale).max()
+    assert np.all(np.tril(r, -1) == 0)
+    return recon, ortho, dr
+
+
+@pytest.mark.parametrize("m,n", [(65, 65), (100, 80), (80, 100), (200, 200), (300, 129), (129, 300), (513, 257)])
+def test_qr_blocked_shapes(cuda, api, oracle, m, n):
+    a = gaussian((2, m, n), m * 1000 + n)
+    q, r = api.qr(a, "reduced")
+    qo, ro = oracle.qr(a, "reduced")
+    q, r = to_np(q), to_np(r)
+    recon, ortho, dr = _qr_check(a, q, r, ro, min(m, n))
+    print(f"[qr {m}x{n}] recon {recon.max():.3e} ortho {ortho.max():.3e} |R| vs LAPACK {dr:.3e}")
+    assert recon.max() <= bound(max(m, n)) and ortho.max() <= bound(max(m, n))
+    assert dr <= 1e-4
+
+
+@pytest.mark.parametrize("mode", ["r", "complete"])
+@pytest.mark.parametrize("m,n", [(150, 100), (100, 150)])
+def test_qr_blocked_modes(cuda, api, oracle, mode, m, n):
+    a = gaussian((1, m, n), 17 + m + n)
+    q, r = api.qr(a, mode)
+    qo, ro = oracle.qr(a, mode)
+    r = to_np(r)
+    assert r.shape == ro.shape
+    if mode == "r":
+        assert q is None
+        _, _, dr = _qr_check(a, None, r, ro, min(m, n))
+    else:
+        q = to_np(q)
+        assert q.shape == (1, m, m)
+        recon, ortho, dr = _qr_check(a, q, r, ro, min(m, n))
+        assert recon.max() <= bound(max(m, n)) and ortho.max() <= bound(max(m, n))
+    assert dr <= 1e-4
+
+
+def test_qr_blocked_special(cuda, api, oracle):
+    m, n = 160, 140
+    a = gaussian((4, m, n), 5)
+    a[1] = np.nan
+    a[2] = 0.0
+    a[3] *= 1e30   # scaled by a power of two inside: no overflow
+    q, r = api.qr(a, "reduced")
+    q, r = to_np(q), to_np(r)
+    assert np.isnan(q[1]).all() and np.isnan(r[1]).all()
+    assert np.isfinite(q[[0, 2, 3]]).all() and np.isfinite(r[[0, 2, 3]]).all()
+    assert np.array_equal(q[2], np.eye(m, n, dtype=np.float32)) and np.all(r[2] == 0)
+    qo, ro = oracle.qr(a[[0, 3]], "reduced")
+    recon, ortho, dr = _qr_check(a[[0, 3]], q[[0, 3]], r[[0, 3]], ro, n)
+    assert recon.max() <= bound(m) and ortho.max() <= bound(m) and dr <= 1e-4
+
+
+def test_config5_qr(cuda, api, oracle):
+    torch = cuda
+    g = config5_matrix()
+    q, r = api.qr(dev(torch, g[None]), "reduced")
+    q, r = to_np(q), to_np(r)
+    qo, ro = oracle.qr(g[None], "reduced")
+    recon, ortho, dr = _qr_check(g[None], q, r, ro, 4096)
+    print(f"[qr config5] recon {recon.max():.3e} ortho {ortho.max():.3e} (bound {bound(4096):.3e}) "
+          f"|R| vs LAPACK {dr:.3e}")
+    assert recon.max() <= bound(4096) and ortho.max() <= bound(4096) and dr <= 1e-4
