@@ -19,9 +19,9 @@
 //                 products of the reflector with the leaf's other columns
 //                 (an LDS transpose-reduction), the update, and the leaf's
 //                 T (T[0:k, k] = -tau_k T[0:k, 0:k] V^T v_k) on the way
-//   sgemm x2      Y = V^T C for the panel's later columns, split over rows
+//   gram          Y = V^T C for the panel's later columns, split over rows
 //   qr_apply      C -= V (T^T Y), one thread per row
-//   qr_panel_t    the panel's 128 x 128 T from the leaves' T and V^T V
+//   qr_panel_t    the panel's 128 x 128 T from the leaves' T and V^T V (gram)
 //   sgemm         W = V^T A2 (split over rows), summed, W = T^T W,
 //                 A2 -= V W: the trailing matrix (MFMA)
 // Q: [I; 0], then per panel from the last: Q2 -= V (T (V^T Q2)).
@@ -348,24 +348,35 @@ __global__ __launch_bounds__(256) void qr_leaf_apply_kernel(float* __restrict__ 
 // ---- the panel's T (nbk x nbk, upper triangular, row-major) ----
 //
 // Diagonal 16 x 16 blocks are the leaves' T; block column j above them is
-// T[0:16j, Bj] = -T[0:16j, 0:16j] (S[0:16j, Bj] T_jj), S = V^T V summed
-// from nsplit partials (nbk x nbk each).
-__global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict__ Spart, int nsplit,
+// T[0:16j, Bj] = -T[0:16j, 0:16j] (S[0:16j, Bj] T_jj), S = V^T V
+// (nbk x nbk, row-major).
+__global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict__ Ssum,
                                                          const float* __restrict__ Tleaves, int nbk,
                                                          float* __restrict__ Tout) {
     __shared__ float S[NB][NB + 1];
     __shared__ float T[NB][NB + 1];
     __shared__ float X[NB][LW + 1];
     const int t = threadIdx.x;
-    for (int idx = t; idx < NB * NB; idx += 256) {
-        const int i = idx >> 7, j = idx & (NB - 1);
-        float s = 0.0f;
-        if (i < nbk && j < nbk && j > i)
-            for (int b = 0; b < nsplit; ++b) s += Spart[(size_t)b * nbk * nbk + (size_t)i * nbk + j];
-        S[i][j] = s;
-        // diagonal blocks from the leaves
-        const int bi = i / LW, bj = j / LW;
-        T[i][j] = (bi == bj && i < nbk && j < nbk) ? Tleaves[(size_t)bi * LW * LW + (i % LW) * LW + (j % LW)] : 0.0f;
+    for (int idx0 = 0; idx0 < NB * NB; idx0 += 256 * 8) {
+        float sv[8], tv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int idx = idx0 + u * 256 + t, i = idx >> 7, j = idx & (NB - 1);
+            const bool in = i < nbk && j < nbk && j > i;
+            const float sx = Ssum[in ? (size_t)i * nbk + j : 0];
+            sv[u] = in ? sx : 0.0f;
+            // diagonal blocks from the leaves
+            const int bi = i / LW, bj = j / LW;
+            const bool din = bi == bj && i < nbk && j < nbk;
+            const float x = Tleaves[din ? (size_t)bi * LW * LW + (i % LW) * LW + (j % LW) : 0];
+            tv[u] = din ? x : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int idx = idx0 + u * 256 + t;
+            S[idx >> 7][idx & (NB - 1)] = sv[u];
+            T[idx >> 7][idx & (NB - 1)] = tv[u];
+        }
     }
     __syncthreads();
     const int nblk = (nbk + LW - 1) / LW;
@@ -412,6 +423,88 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
 void transpose(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s) {
     hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32)), dim3(256), 0, s, src,
                        lds, dst, ldd, rows, cols);
+}
+
+// Products of row vectors over a split of their length:
+//   part[b][i][j] = sum_{r in chunk b} X[i][r] Y[j][r]
+// (X: M rows, Y: N rows, both with row stride ld, entries 0 .. K - 1;
+// chunks of kChunk).  For the thin products of the panel -- V^T C with 16
+// reflectors, V^T V -- whose outputs are too few for matrix-core tiles:
+// a workgroup takes 16 x 16 outputs of one chunk, both operands' slices
+// staged in LDS, one output per thread, four entries per LDS read.
+constexpr int kGramTile = 16;
+
+__global__ __launch_bounds__(256) void gram_kernel(const float* __restrict__ X, const float* __restrict__ Y, int ld,
+                                                   int M, int N, int K, float* __restrict__ part) {
+    __shared__ float xs[kGramTile][kChunk + 4];
+    __shared__ float ys[kGramTile][kChunk + 4];
+    const int t = threadIdx.x;
+    const int i0 = blockIdx.x * kGramTile, j0 = blockIdx.y * kGramTile, b = blockIdx.z;
+    const int r0 = b * kChunk;
+    const int len = min(kChunk, K - r0);
+    // stage: 16 rows x kChunk of each operand; 4-float groups, clamped loads
+    const bool vec = (ld & 3) == 0 && (((uintptr_t)X | (uintptr_t)Y) & 15) == 0;
+    constexpr int groups = kGramTile * kChunk / 4;   // 2048 per operand
+#pragma unroll
+    for (int g0 = 0; g0 < groups; g0 += 256 * 4) {
+        float4 xv[4], yv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = g0 + u * 256 + t, row = g / (kChunk / 4), c4 = (g % (kChunk / 4)) * 4;
+            const bool xin = i0 + row < M, yin = j0 + row < N;
+            const size_t xo = (size_t)(xin ? i0 + row : 0) * ld + r0 + c4;
+            const size_t yo = (size_t)(yin ? j0 + row : 0) * ld + r0 + c4;
+            if (vec && c4 + 3 < len) {
+                xv[u] = *reinterpret_cast<const float4*>(X + xo);
+                yv[u] = *reinterpret_cast<const float4*>(Y + yo);
+            } else {
+                float xx[4], yy[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool in = c4 + e < len;
+                    xx[e] = X[in ? xo + e : 0];
+                    yy[e] = Y[in ? yo + e : 0];
+                    xx[e] = in ? xx[e] : 0.0f;
+                    yy[e] = in ? yy[e] : 0.0f;
+                }
+                xv[u] = make_float4(xx[0], xx[1], xx[2], xx[3]);
+                yv[u] = make_float4(yy[0], yy[1], yy[2], yy[3]);
+            }
+            if (!xin) xv[u] = make_float4(0, 0, 0, 0);
+            if (!yin) yv[u] = make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int g = g0 + u * 256 + t, row = g / (kChunk / 4), c4 = (g % (kChunk / 4)) * 4;
+            *reinterpret_cast<float4*>(&xs[row][c4]) = xv[u];
+            *reinterpret_cast<float4*>(&ys[row][c4]) = yv[u];
+        }
+    }
+    __syncthreads();
+    const int i = t >> 4, j = t & 15;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int r = 0; r < kChunk; r += 8) {
+        const float4 a0 = *reinterpret_cast<const float4*>(&xs[i][r]);
+        const float4 b0 = *reinterpret_cast<const float4*>(&ys[j][r]);
+        const float4 a1 = *reinterpret_cast<const float4*>(&xs[i][r + 4]);
+        const float4 b1 = *reinterpret_cast<const float4*>(&ys[j][r + 4]);
+        acc0 = fmaf(a0.x, b0.x, acc0);
+        acc1 = fmaf(a1.x, b1.x, acc1);
+        acc0 = fmaf(a0.y, b0.y, acc0);
+        acc1 = fmaf(a1.y, b1.y, acc1);
+        acc0 = fmaf(a0.z, b0.z, acc0);
+        acc1 = fmaf(a1.z, b1.z, acc1);
+        acc0 = fmaf(a0.w, b0.w, acc0);
+        acc1 = fmaf(a1.w, b1.w, acc1);
+    }
+    if (i0 + i < M && j0 + j < N) part[(size_t)b * M * N + (size_t)(i0 + i) * N + j0 + j] = acc0 + acc1;
+}
+
+int gram(const float* X, const float* Y, int ld, int M, int N, int K, float* part, hipStream_t s) {
+    const int nsplit = cdiv(K, kChunk);
+    hipLaunchKernelGGL(gram_kernel, dim3((unsigned)cdiv(M, kGramTile), (unsigned)cdiv(N, kGramTile), (unsigned)nsplit),
+                       dim3(256), 0, s, X, Y, ld, M, N, K, part);
+    return nsplit;
 }
 
 // out[i] = sum_b part[b][i]
@@ -550,8 +643,8 @@ void qr_blocked_one(const float* a, float* q, float* r, int m, int n, int qc, in
                 if (ncol > 0) {
                     // Y = V^T C over the leaf's rows, then C -= V (T^T Y)
                     const int rows = ldp - cl;
-                    const int nsplit = split_k_gemm(true, lw, ncol, rows, Vt + (size_t)cl * ldv + cl, ldv,
-                                                    w.P + (size_t)(cl + lw) * ldp + cl, ldp, w.part, s);
+                    const int nsplit = gram(Vt + (size_t)cl * ldv + cl, w.P + (size_t)(cl + lw) * ldp + cl, ldp, lw,
+                                            ncol, rows, w.part, s);
                     hipLaunchKernelGGL(qr_leaf_apply_kernel,
                                        dim3((unsigned)cdiv(rows, 256), (unsigned)cdiv(ncol, kApplyCols)), dim3(256),
                                        0, s, w.P, ldp, cl, lw, ncol, Vt, ldv, w.part, nsplit,
@@ -564,8 +657,10 @@ void qr_blocked_one(const float* a, float* q, float* r, int m, int n, int qc, in
         // the panel's T from the leaves' T and S = V^T V
         float* T = w.T + (size_t)pi * NB * NB;
         {
-            const int nsplit = split_k_gemm(true, nbk, nbk, ldp, Vt, ldv, Vt, ldv, w.part, s);
-            hipLaunchKernelGGL(qr_panel_t_kernel, dim3(1), dim3(256), 0, s, w.part, nsplit, w.Tleaves, nbk, T);
+            const int nsplit = gram(Vt, Vt, ldv, nbk, nbk, ldp, w.part, s);
+            hipLaunchKernelGGL(sum_parts_kernel, dim3(grid_for((size_t)nbk * nbk)), dim3(256), 0, s, w.part, nsplit,
+                               (size_t)nbk * nbk, w.W);
+            hipLaunchKernelGGL(qr_panel_t_kernel, dim3(1), dim3(256), 0, s, w.W, w.Tleaves, nbk, T);
         }
         // trailing matrix: A2 -= V (T^T (V^T A2))
         const int n2 = n - pe;
