@@ -48,8 +48,12 @@ struct GemmArgs {
 // Loads this thread's share of a 128 x 16 operand tile (rows r0.., k0..) into
 // registers: 2048 floats = 256 threads x 8.  TRANS = the operand is stored
 // k-major (element (row, k) at p[k * ld + row]): op(A) = A^T, and op(B) = B
-// (whose tile rows are B's columns).
-template <bool TRANS>
+// (whose tile rows are B's columns).  VEC: 16-byte aligned rows and a
+// contiguous extent that is a multiple of 4, so a float4 is wholly inside
+// or wholly outside.  Every load is issued unconditionally (outside the
+// operand: from its first element, then masked to zero), so that no branch
+// join forces a wait on the prefetch.
+template <bool TRANS, bool VEC>
 __device__ __forceinline__ void load_tile(const float* __restrict__ p, int ld, int rows, int K, int r0, int k0,
                                           float (&reg)[8]) {
     const int t = threadIdx.x;
@@ -60,16 +64,18 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ p, int ld, i
         for (int h = 0; h < 2; ++h) {
             const int r = r0 + (t >> 2) + h * 64;
             const int k = k0 + kq;
-            if (r < rows && k + 3 < K && (((uintptr_t)(p + (size_t)r * ld + k)) & 15) == 0) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (size_t)r * ld + k);
-                reg[h * 4 + 0] = v[0];
-                reg[h * 4 + 1] = v[1];
-                reg[h * 4 + 2] = v[2];
-                reg[h * 4 + 3] = v[3];
+            if (VEC) {
+                const bool in = r < rows && k < K;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)r * ld + k : 0));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) reg[h * 4 + i] = in ? v[i] : 0.0f;
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    reg[h * 4 + i] = (r < rows && k + i < K) ? p[(size_t)r * ld + k + i] : 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    const bool in = r < rows && k + i < K;
+                    const float x = p[in ? (size_t)r * ld + k + i : 0];
+                    reg[h * 4 + i] = in ? x : 0.0f;
+                }
             }
         }
     } else {
@@ -80,16 +86,18 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ p, int ld, i
         for (int h = 0; h < 2; ++h) {
             const int k = k0 + (t >> 5) + h * 8;
             const int r = r0 + rq;
-            if (k < K && r + 3 < rows && (((uintptr_t)(p + (size_t)k * ld + r)) & 15) == 0) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (size_t)k * ld + r);
-                reg[h * 4 + 0] = v[0];
-                reg[h * 4 + 1] = v[1];
-                reg[h * 4 + 2] = v[2];
-                reg[h * 4 + 3] = v[3];
+            if (VEC) {
+                const bool in = k < K && r < rows;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)k * ld + r : 0));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) reg[h * 4 + i] = in ? v[i] : 0.0f;
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    reg[h * 4 + i] = (k < K && r + i < rows) ? p[(size_t)k * ld + r + i] : 0.0f;
+                for (int i = 0; i < 4; ++i) {
+                    const bool in = k < K && r + i < rows;
+                    const float x = p[in ? (size_t)k * ld + r + i : 0];
+                    reg[h * 4 + i] = in ? x : 0.0f;
+                }
             }
         }
     }
@@ -118,7 +126,7 @@ __device__ __forceinline__ void store_tile(float (*s)[LP], const float (&reg)[8]
     }
 }
 
-template <bool TA, bool TB>
+template <bool TA, bool TB, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     __shared__ float As[2][BM][LP];
     __shared__ float Bs[2][BN][LP];
@@ -142,8 +150,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     float ra[8], rb[8];
-    load_tile<TA>(A, g.lda, g.M, g.K, m0, 0, ra);
-    load_tile<!TB>(B, g.ldb, g.N, g.K, n0, 0, rb);
+    load_tile<TA, VEC>(A, g.lda, g.M, g.K, m0, 0, ra);
+    load_tile<!TB, VEC>(B, g.ldb, g.N, g.K, n0, 0, rb);
     store_tile<TA>(As[0], ra);
     store_tile<!TB>(Bs[0], rb);
     __syncthreads();
@@ -153,10 +161,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const int kh = (lane >> 5) * 8;   // this lane's 8 k values of the tile
     for (int kt = 0; kt < ktiles; ++kt) {
         const int cur = kt & 1;
-        if (kt + 1 < ktiles) {
-            load_tile<TA>(A, g.lda, g.M, g.K, m0, (kt + 1) * BK, ra);
-            load_tile<!TB>(B, g.ldb, g.N, g.K, n0, (kt + 1) * BK, rb);
-        }
+        // the next tile (past the end: all masked, no branch)
+        load_tile<TA, VEC>(A, g.lda, g.M, g.K, m0, (kt + 1) * BK, ra);
+        load_tile<!TB, VEC>(B, g.ldb, g.N, g.K, n0, (kt + 1) * BK, rb);
         floatx4 a0[2][2], b0[2][2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -174,28 +181,37 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[i][s >> 2][s & 3], b0[j][s >> 2][s & 3],
                                                                      acc[i][j], 0, 0, 0);
         }
-        if (kt + 1 < ktiles) {
-            store_tile<TA>(As[cur ^ 1], ra);
-            store_tile<!TB>(Bs[cur ^ 1], rb);
-        }
+        store_tile<TA>(As[cur ^ 1], ra);   // (after the last tile: zeros, never read)
+        store_tile<!TB>(Bs[cur ^ 1], rb);
         __syncthreads();
     }
 
     // epilogue: lane holds column (lane & 31) of each 32 x 32 block, rows
-    // 8 * (e / 4) + 4 * (lane / 32) + (e % 4)
+    // 8 * (e / 4) + 4 * (lane / 32) + (e % 4).  Per block, the 16 loads of C
+    // (clamped addresses) are all issued before the first use, so that their
+    // latencies overlap instead of adding up.
+    const bool keep = g.beta != 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int col = n0 + wn + j * 32 + lr;
-            if (col >= g.N) continue;
+            const bool cin = col < g.N;
+            float cv[16];
+            if (keep) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                    const bool in = cin && row < g.M;
+                    cv[e] = C[in ? (size_t)row * g.ldc + col : 0];
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < g.M) {
-                    float* cp = C + (size_t)row * g.ldc + col;
+                if (cin && row < g.M) {
                     const float v = g.alpha * acc[i][j][e];
-                    *cp = g.beta == 0.0f ? v : fmaf(g.beta, *cp, v);
+                    C[(size_t)row * g.ldc + col] = keep ? fmaf(g.beta, cv[e], v) : v;
                 }
             }
         }
@@ -210,10 +226,21 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
     GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta, lower_only ? 1 : 0};
     const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
     KernelTimer t("gemm_mfma", s);
-    if (!ta && !tb) hipLaunchKernelGGL((gemm_kernel<false, false>), grid, dim3(256), 0, s, g);
-    else if (!ta && tb) hipLaunchKernelGGL((gemm_kernel<false, true>), grid, dim3(256), 0, s, g);
-    else if (ta && !tb) hipLaunchKernelGGL((gemm_kernel<true, false>), grid, dim3(256), 0, s, g);
-    else hipLaunchKernelGGL((gemm_kernel<true, true>), grid, dim3(256), 0, s, g);
+    // float4 operand loads: 16-byte aligned bases, strides and leading
+    // dimensions, and the contiguous extent of each operand a multiple of 4
+    auto al = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
+    const bool vec = al(A) && al(B) && (lda & 3) == 0 && (ldb & 3) == 0 && (sa & 3) == 0 && (sb & 3) == 0 &&
+                     ((ta ? M : K) & 3) == 0 && ((tb ? K : N) & 3) == 0;
+#define MLA_GEMM_LAUNCH(TA_, TB_)                                                                       \
+    do {                                                                                                \
+        if (vec) hipLaunchKernelGGL((gemm_kernel<TA_, TB_, true>), grid, dim3(256), 0, s, g);           \
+        else hipLaunchKernelGGL((gemm_kernel<TA_, TB_, false>), grid, dim3(256), 0, s, g);              \
+    } while (0)
+    if (!ta && !tb) MLA_GEMM_LAUNCH(false, false);
+    else if (!ta && tb) MLA_GEMM_LAUNCH(false, true);
+    else if (ta && !tb) MLA_GEMM_LAUNCH(true, false);
+    else MLA_GEMM_LAUNCH(true, true);
+#undef MLA_GEMM_LAUNCH
     t.stop();
     MLA_HIP(hipGetLastError());
 }
