@@ -38,6 +38,12 @@ int metal_linalg_hip_sgemm(int transa, int transb, int M, int N, int K, float al
                            long long stride_a, const float* B, int ldb, long long stride_b, float beta, float* C,
                            int ldc, long long stride_c, int batch);
 
+/* The tridiagonal form T = Q^T A Q of one symmetric n x n matrix (the lower
+ * triangle read if `lower`, else the upper), as used by the large-matrix
+ * eigh: d (n) and e (n - 1), host or device pointers.  Returns a
+ * metal_linalg_status value.  For tests. */
+int metal_linalg_hip_sytrd(const float* a, uint32_t n, int lower, float* d, float* e);
+
 /* The device's gcnArchName ("" without a GPU). */
 const char* metal_linalg_hip_arch(void);
 

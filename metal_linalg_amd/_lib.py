@@ -96,6 +96,7 @@ hip_arch = _fn("metal_linalg_hip_arch", _cstr)
 _ll = ctypes.c_longlong
 hip_sgemm = _fn("metal_linalg_hip_sgemm", _int, _int, _int, _int, _int, _int, ctypes.c_float, _p, _int, _ll, _p, _int,
                 _ll, ctypes.c_float, _p, _int, _ll, _int)
+hip_sytrd = _fn("metal_linalg_hip_sytrd", _int, _p, _u32, _int, _p, _p)
 
 
 def _struct(name, fields):

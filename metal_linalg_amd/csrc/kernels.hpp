@@ -62,6 +62,19 @@ bool eigh_small_fits(uint32_t n);
 void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
                 hipStream_t s);
 
+// ---- symmetric eigendecomposition for larger n (<= 16384), one matrix at a time ----
+struct EighWork {
+    float *A, *V, *W, *abuf, *y, *partA, *partB, *d, *e, *tau;
+    uint32_t* flags;   // [0] bits of max |a| over the read triangle, [1] non-finite
+    float* rest;       // what follows stage 1's part of the workspace
+};
+bool eigh_blocked_fits(uint32_t n);
+size_t eigh_sytrd_floats(uint32_t n);                 // stage 1's part of the workspace
+EighWork eigh_carve(float* base, uint32_t n);
+void sytrd_one(const float* a, uint32_t n, bool lower, const EighWork& w, hipStream_t s);
+// y = x * 2^e (the scale stage 1 took out), or NaN for a non-finite matrix
+void eigh_unscale(const float* x, float* y, uint32_t count, const uint32_t* flags, hipStream_t s);
+
 // ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128 ----
 bool svd_small_fits(uint32_t m, uint32_t n);
 size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes

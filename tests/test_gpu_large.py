@@ -260,3 +260,35 @@ def test_config5_qr(cuda, api, oracle):
     print(f"[qr config5] recon {recon.max():.3e} ortho {ortho.max():.3e} (bound {bound(4096):.3e}) "
           f"|R| vs LAPACK {dr:.3e}")
     assert recon.max() <= bound(4096) and ortho.max() <= bound(4096) and dr <= 1e-4
+
+
+# ---- eigh (beyond 64: the blocked path) ----
+
+def _sytrd(torch, a, lower=True):
+    from metal_linalg_amd import _lib
+
+    n = a.shape[-1]
+    ta = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    d = torch.empty(n, dtype=torch.float32, device="cuda")
+    e = torch.empty(n - 1, dtype=torch.float32, device="cuda")
+    assert _lib.hip_sytrd(ta.data_ptr(), n, int(lower), d.data_ptr(), e.data_ptr()) == 0
+    return d.cpu().numpy().astype(np.float64), e.cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("n", [65, 100, 128, 129, 200, 513])
+@pytest.mark.parametrize("lower", [True, False])
+def test_sytrd_spectrum(cuda, oracle, n, lower):
+    """T = Q^T A Q keeps A's spectrum: eigenvalues of (d, e) against LAPACK's."""
+    from scipy.linalg import eigh_tridiagonal
+
+    g = gaussian((n, n), 900 + n)
+    a = ((g + g.T) / 2).astype(np.float32)
+    junk = a.copy()
+    iu = np.triu_indices(n, 1) if lower else np.tril_indices(n, -1)
+    junk[iu] = np.nan   # the unread triangle
+    d, e = _sytrd(cuda, junk, lower)
+    wt = eigh_tridiagonal(d, e, eigvals_only=True)
+    wo, _, _ = oracle.eigh(a[None], lower, False)
+    rel = np.abs(np.sort(wt) - wo[0].astype(np.float64)).max() / np.abs(wo[0]).max()
+    print(f"[sytrd n={n} lower={lower}] eigenvalues of T vs LAPACK: {rel:.3e}")
+    assert rel <= 1e-5
