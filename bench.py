@@ -188,6 +188,27 @@ def workloads():
             f += 4 * rows * b * n2 + 4 * rows * b * nq
         return f
 
+    def eigh5_make():
+        g = U.config5_matrix()
+        return {"a": ((g.astype(np.float64) + g.T) / 2).astype(np.float32)}
+
+    def eigh_gemm_flops(n, nb=64):
+        # the matrix-core products: the reduction's trailing updates
+        # (A22 -= V W^T + W V^T per panel), the Newton-Schulz step (Z^T Z and
+        # Z M) and the back-transformation (V^T Z2 and Z2 -= V W2 per panel)
+        f = 4 * n ** 3
+        for j0 in range(0, n - 1, nb):
+            b = min(nb, n - 1 - j0)
+            n2 = n - min(j0 + nb, n)
+            f += 4 * n2 * n2 * nb + 4 * (n - j0 - 1) * b * n
+        return f
+
+    w["eigh4096"] = Workload(
+        "eigh4096", "eigh lower with vectors, one 4096x4096 fp32 (G + G^T)/2, G ~ N(0,1) (BASELINE config 5)", 1,
+        eigh5_make, lambda api, t: api.eigh(t["a"], True, True), "gemm_mfma", None, eigh_gemm_flops(n5), "mfma",
+        lambda o, h, n: o.eigh(h["a"][None], True, True), {"n": n5}, unit="GFLOP/s",
+        nominal_flops=(4 * n5 ** 3) // 3 + 2 * n5 ** 3)
+
     w["qr4096"] = Workload(
         "qr4096", "qr_with_mode reduced, one 4096x4096 fp32 G ~ N(0,1) (BASELINE config 5)", 1, qr5_make,
         lambda api, t: api.qr(t["a"], "reduced"), "gemm_mfma", None, qr_gemm_flops(n5), "mfma",

@@ -109,15 +109,27 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
         }
         return;
     }
-    if (!eigh_small_fits(n))
-        invalid("[eigh] n = " + std::to_string(n) + ": this build's eigh kernels take n <= 64 so far");
+    const bool small = eigh_small_fits(n);
+    if (!small && !eigh_blocked_fits(n))
+        invalid("[eigh] n = " + std::to_string(n) + ": this build's eigh kernels take n <= 16384");
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dw = call.out(w, (size_t)B * n);
     float* dv = v ? call.out(v, (size_t)B * n * n) : nullptr;
     uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
-    eigh_small(da, dw, dv, di, B, n, lower, call.stream());
-    check_converged(di, B, call.stream(), "eigh");
+    if (small) {
+        eigh_small(da, dw, dv, di, B, n, lower, call.stream());
+        check_converged(di, B, call.stream(), "eigh");
+    } else {
+        const size_t floats = eigh_sytrd_floats(n) + eigh_tridiag_floats(n);
+        float* work = static_cast<float*>(call.scratch(floats * sizeof(float)));
+        const EighWork ew = eigh_carve(work, n);
+        const size_t per = (size_t)n * n;
+        for (uint32_t b = 0; b < B; ++b) {
+            sytrd_one(da + b * per, n, lower, ew, call.stream());
+            eigh_tridiag_one(ew, n, dw + (size_t)b * n, dv ? dv + b * per : nullptr, di + b, call.stream());
+        }
+    }
     call.finish();
 }
 

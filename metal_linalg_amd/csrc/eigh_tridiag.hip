@@ -1,0 +1,465 @@
+// Stages 2 and 3 of the large-matrix eigh: the tridiagonal eigenproblem
+// T = Z diag(w) Z^T, and the back-transformation V = Q Z.
+//
+// Role: the MI355X counterpart of the reference's tridiagonal solver and
+// back-transform (reference: src/divide_conquer.cpp:934
+// tridiagonal_eigensystem, src/svd_bidiag.mm eigh_band_vectors V = Q1 Q2 Z);
+// LAPACK's contract for the result (ssyevd: ascending eigenvalues,
+// orthonormal eigenvectors).  The method is LAPACK's other route, sstebz +
+// sstein, shaped for a GPU:
+//   - T splits where |e_i| <= eps sqrt(|d_i d_{i+1}|) into unreduced blocks
+//     (their eigenvectors have disjoint supports);
+//   - eigenvalues by multisection of the Sturm count: 16 lanes per
+//     eigenvalue evaluate 16 points at once, so an iteration narrows the
+//     interval 17-fold (sstebz bisects);
+//   - eigenvectors by inverse iteration from a pseudo-random start, three
+//     solves with (T - lambda I) factored with partial pivoting (slagtf /
+//     slagts), one thread per cluster of eigenvalues closer than
+//     1e-5 ||T||, modified Gram-Schmidt inside a cluster (sstein);
+//   - the remaining loss of orthogonality (of order eps ||T|| / gap) removed
+//     by one Newton-Schulz step Z <- Z (3 I - Z^T Z) / 2 on the matrix
+//     cores: the columns move by a skew-symmetric correction of the same
+//     order, which changes the residual A Z - Z W only at the eps ||T||
+//     level;
+//   - V = Q Z with Q's reflectors in compact WY form per panel of 64:
+//     Z2 -= V (T (V^T Z2)), MFMA products.
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+#include <vector>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "runtime.hpp"
+
+namespace mla {
+namespace {
+
+constexpr int NBT = 64;        // the reduction's panel width (reflectors per block)
+constexpr int kMS = 16;        // multisection points per eigenvalue
+constexpr int kIters = 3;      // inverse-iteration solves
+
+struct Slot {            // one eigenvalue: its block and its place in it
+    int start, size, local, pad;
+    float lo, hi;        // the block's Gershgorin interval
+};
+
+// ---- eigenvalues: multisection of the Sturm count ----
+//
+// count(x) = the number of eigenvalues of the block below x, from the signs
+// of the pivots of T - x I = L D L^T (q_i = d_i - x - e_{i-1}^2 / q_{i-1});
+// a pivot smaller than pivmin in magnitude is taken as -pivmin.
+__device__ __forceinline__ int sturm_count(const float* __restrict__ d, const float* __restrict__ e2, int s, int m,
+                                           float x, float pivmin) {
+    float q = d[s] - x;
+    q = fabsf(q) <= pivmin ? -pivmin : q;
+    int c = q < 0.0f;
+    for (int i = 1; i < m; ++i) {
+        q = (d[s + i] - x) - e2[s + i - 1] * __builtin_amdgcn_rcpf(q);
+        q = fabsf(q) <= pivmin ? -pivmin : q;
+        c += q < 0.0f;
+    }
+    return c;
+}
+
+__global__ __launch_bounds__(256) void multisection_kernel(const float* __restrict__ d, const float* __restrict__ e2,
+                                                           const Slot* __restrict__ slots, int nslots, float pivmin,
+                                                           float* __restrict__ lam) {
+    const int t = threadIdx.x, lane = t & 63;
+    const int sidx = blockIdx.x * (256 / kMS) + (t / kMS);
+    const int j = t % kMS;   // this lane's point
+    const bool live = sidx < nslots;
+    const Slot sl = slots[live ? sidx : 0];
+    float lo = sl.lo, hi = sl.hi;
+    for (int it = 0; it < 12; ++it) {
+        const float x = lo + (hi - lo) * (float)(j + 1) / (float)(kMS + 1);
+        const bool above = live && sturm_count(d, e2, sl.start, sl.size, x, pivmin) > sl.local;
+        // the first point (of this eigenvalue's 16) with more than `local`
+        // eigenvalues below it bounds the eigenvalue from above
+        const unsigned long long b = __ballot(above);
+        const unsigned row = (unsigned)(b >> ((lane / kMS) * kMS)) & ((1u << kMS) - 1u);
+        const int first = row ? __ffs(row) - 1 : kMS;
+        const float nlo = first == 0 ? lo : lo + (hi - lo) * (float)first / (float)(kMS + 1);
+        const float nhi = first == kMS ? hi : lo + (hi - lo) * (float)(first + 1) / (float)(kMS + 1);
+        lo = nlo;
+        hi = nhi;
+        if (hi - lo <= 2.0f * FLT_EPSILON * fmaxf(fabsf(lo), fabsf(hi)) + pivmin) break;   // uniform per 16 lanes
+    }
+    if (live && j == 0) lam[sidx] = 0.5f * (lo + hi);
+}
+
+// ---- eigenvectors: inverse iteration ----
+
+struct Cluster {         // consecutive slots of one block, close together
+    int start, size;     // the block
+    int first, count;    // slots first .. first + count - 1
+};
+
+__device__ __forceinline__ float hash_uniform(unsigned a, unsigned b) {
+    unsigned x = a * 0x9E3779B1u ^ (b + 0x7F4A7C15u) * 0x85EBCA77u;
+    x ^= x >> 15;
+    x *= 0x2C1B3C6Du;
+    x ^= x >> 12;
+    x *= 0x297A2D39u;
+    x ^= x >> 15;
+    return (float)(x >> 8) * (2.0f / 16777216.0f) - 1.0f;   // (-1, 1)
+}
+
+// One thread per cluster.  Z[r * ldz + slot] holds the vectors (rows of
+// the block; the thread also zeroes the rest of its columns).  U is scratch
+// for the factor: 3 floats per row, [3 * row][thread] (coalesced).
+__global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __restrict__ d,
+                                                                const float* __restrict__ e,
+                                                                const Cluster* __restrict__ cl, int ncl,
+                                                                const float* __restrict__ lam, float tnorm,
+                                                                float* __restrict__ Z, int ldz, int n,
+                                                                float* __restrict__ U) {
+    const int tid = blockIdx.x * 256 + threadIdx.x;
+    if (tid >= ncl) return;
+    const Cluster c = cl[tid];
+    const int s = c.start, m = c.size;
+    float* u0 = U + tid;            // U[(3 r + 0) * ncl + tid]
+    const size_t us = (size_t)ncl;
+    const float tol = FLT_EPSILON * tnorm;   // a zero pivot becomes this
+    for (int q = 0; q < c.count; ++q) {
+        const int slot = c.first + q;
+        float* z = Z + slot;        // z[r * ldz]
+        // zero outside the block
+        for (int r = 0; r < s; ++r) z[(size_t)r * ldz] = 0.0f;
+        for (int r = s + m; r < n; ++r) z[(size_t)r * ldz] = 0.0f;
+        if (m == 1) {
+            z[(size_t)s * ldz] = 1.0f;
+            continue;
+        }
+        const float lambda = lam[slot];
+        for (int r = 0; r < m; ++r) z[(size_t)(s + r) * ldz] = hash_uniform((unsigned)slot, (unsigned)r);
+        for (int it = 0; it < kIters; ++it) {
+            // forward: factor (T - lambda I) = P L U on the fly, apply P, L to z
+            float a = d[s] - lambda;         // the running diagonal entry of row k
+            float cc = e[s];                 // row k's superdiagonal
+            float b0 = z[(size_t)s * ldz];   // the running right-hand side of row k
+            for (int k = 0; k < m - 1; ++k) {
+                const float bk = e[s + k];           // subdiagonal (row k + 1, column k)
+                const float an = d[s + k + 1] - lambda;
+                const float cn = k + 1 < m - 1 ? e[s + k + 1] : 0.0f;
+                const float b1 = z[(size_t)(s + k + 1) * ldz];
+                float p0, p1, p2, nb0, na, nc, rhs;
+                if (fabsf(a) >= fabsf(bk)) {
+                    const float l = a == 0.0f ? 0.0f : bk / a;
+                    p0 = a;
+                    p1 = cc;
+                    p2 = 0.0f;
+                    rhs = b0;
+                    na = an - l * cc;
+                    nc = cn;
+                    nb0 = b1 - l * b0;
+                } else {
+                    const float l = a / bk;
+                    p0 = bk;
+                    p1 = an;
+                    p2 = cn;
+                    rhs = b1;
+                    na = cc - l * an;
+                    nc = -l * cn;
+                    nb0 = b0 - l * b1;
+                }
+                if (p0 == 0.0f) p0 = tol;
+                u0[(3 * (size_t)k + 0) * us] = p0;
+                u0[(3 * (size_t)k + 1) * us] = p1;
+                u0[(3 * (size_t)k + 2) * us] = p2;
+                z[(size_t)(s + k) * ldz] = rhs;
+                a = na;
+                cc = nc;
+                b0 = nb0;
+            }
+            if (a == 0.0f) a = tol;
+            // backward: U x = rhs, and |x|^2
+            float x2 = 0.0f, x1 = 0.0f, nrm = 0.0f;
+            {
+                const float x = b0 / a;
+                z[(size_t)(s + m - 1) * ldz] = x;
+                x1 = x;
+                nrm = x * x;
+            }
+            for (int k = m - 2; k >= 0; --k) {
+                const float p0 = u0[(3 * (size_t)k + 0) * us];
+                const float p1 = u0[(3 * (size_t)k + 1) * us];
+                const float p2 = u0[(3 * (size_t)k + 2) * us];
+                const float x = (z[(size_t)(s + k) * ldz] - p1 * x1 - p2 * x2) / p0;
+                z[(size_t)(s + k) * ldz] = x;
+                x2 = x1;
+                x1 = x;
+                nrm = fmaf(x, x, nrm);
+            }
+            // against the cluster's earlier vectors (modified Gram-Schmidt)
+            for (int p = 0; p < q; ++p) {
+                const float* zp = Z + c.first + p;
+                float dot = 0.0f;
+                for (int r = 0; r < m; ++r) dot = fmaf(zp[(size_t)(s + r) * ldz], z[(size_t)(s + r) * ldz], dot);
+                nrm = 0.0f;
+                for (int r = 0; r < m; ++r) {
+                    const float x = fmaf(-dot, zp[(size_t)(s + r) * ldz], z[(size_t)(s + r) * ldz]);
+                    z[(size_t)(s + r) * ldz] = x;
+                    nrm = fmaf(x, x, nrm);
+                }
+            }
+            const float inv = nrm > 0.0f ? 1.0f / sqrtf(nrm) : 0.0f;
+            for (int r = 0; r < m; ++r) z[(size_t)(s + r) * ldz] *= inv;
+        }
+    }
+}
+
+// M = (3 I - G) / 2
+__global__ __launch_bounds__(256) void newton_schulz_kernel(float* __restrict__ G, int n) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)n * n) return;
+    const int i = (int)(idx / n), j = (int)(idx - (size_t)i * n);
+    G[idx] = (i == j ? 1.5f : 0.0f) - 0.5f * G[idx];
+}
+
+// T (nb x nb, upper, row-major) of the compact WY form of nb reflectors
+// from S = V^T V (nb x nb) and tau: T[k][k] = tau_k,
+// T[0:k, k] = -tau_k T[0:k, 0:k] S[0:k, k].  One workgroup of 64 threads.
+__global__ __launch_bounds__(64) void wy_t_kernel(const float* __restrict__ S, const float* __restrict__ tau, int nb,
+                                                  float* __restrict__ T) {
+    __shared__ float Ts[NBT][NBT + 1];
+    __shared__ float Ss[NBT][NBT + 1];
+    const int t = threadIdx.x;
+    for (int idx = t; idx < NBT * NBT; idx += 64) {
+        const int i = idx / NBT, j = idx % NBT;
+        Ss[i][j] = (i < nb && j < nb) ? S[i * nb + j] : 0.0f;
+        Ts[i][j] = 0.0f;
+    }
+    __syncthreads();
+    for (int k = 0; k < nb; ++k) {
+        const float tk = tau[k];
+        float s = 0.0f;
+        if (t < k)
+            for (int l = t; l < k; ++l) s = fmaf(Ts[t][l], Ss[l][k], s);
+        __syncthreads();
+        if (t < k) Ts[t][k] = -tk * s;
+        if (t == k) Ts[k][k] = tk;
+        __syncthreads();
+    }
+    for (int idx = t; idx < nb * nb; idx += 64) T[idx] = Ts[idx / nb][idx % nb];
+}
+
+// out[i][j] = Z[i][perm[j]]; w[j] = lam[perm[j]] 2^e
+__global__ __launch_bounds__(256) void permute_columns_kernel(const float* __restrict__ Z, float* __restrict__ V,
+                                                              const int* __restrict__ perm, int n) {
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)n * n) return;
+    const int i = (int)(idx / n), j = (int)(idx - (size_t)i * n);
+    V[idx] = Z[(size_t)i * n + perm[j]];
+}
+
+__global__ __launch_bounds__(256) void permute_values_kernel(const float* __restrict__ lam, float* __restrict__ w,
+                                                             const int* __restrict__ perm, int n,
+                                                             const uint32_t* __restrict__ flags) {
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    if (j >= n) return;
+    const int e = scale_exponent(__uint_as_float(flags[0]));
+    w[j] = ldexpf(lam[perm[j]], e);
+}
+
+__global__ __launch_bounds__(256) void fill_nan_kernel(float* __restrict__ x, size_t count) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) x[i] = qnan();
+}
+
+__global__ __launch_bounds__(256) void sum_parts2_kernel(const float* __restrict__ part, int nsplit, size_t count,
+                                                         float* __restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
+        float s = 0.0f;
+        for (int b = 0; b < nsplit; ++b) s += part[(size_t)b * count + i];
+        out[i] = s;
+    }
+}
+
+__global__ void set_info_kernel(uint32_t* info, const uint32_t* flags) {
+    *info = flags[1] ? (1u << 17) : (1u | (1u << 16));
+}
+
+unsigned grid_of(size_t count) { return (unsigned)std::min<size_t>(cdiv(count, 256), 4096); }
+
+constexpr int kRowChunk = 512;
+
+// C (M x N) = A B over a long K, split in chunks summed afterwards (the
+// products with V^T over many rows): A M x K (row-major, lda); B K x N
+// (ldb), or with tb stored N x K
+void split_rows_gemm(bool tb, int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* part,
+                     float* C, hipStream_t s) {
+    const int full = K / kRowChunk, rest = K - full * kRowChunk;
+    const long long sb = tb ? kRowChunk : (long long)kRowChunk * ldb;
+    if (full > 0)
+        sgemm(false, tb, M, N, kRowChunk, 1.0f, A, lda, kRowChunk, B, ldb, sb, 0.0f, part, N, (long long)M * N, full,
+              s);
+    if (rest > 0)
+        sgemm(false, tb, M, N, rest, 1.0f, A + (size_t)full * kRowChunk, lda, 0,
+              B + (tb ? (size_t)full * kRowChunk : (size_t)full * kRowChunk * ldb), ldb, 0, 0.0f,
+              part + (size_t)full * M * N, N, 0, 1, s);
+    const int nsplit = full + (rest > 0 ? 1 : 0);
+    hipLaunchKernelGGL(sum_parts2_kernel, dim3(grid_of((size_t)M * N)), dim3(256), 0, s, part, nsplit, (size_t)M * N,
+                       C);
+}
+
+}  // namespace
+
+size_t eigh_tridiag_floats(uint32_t n) {
+    const size_t N = n;
+    // lam, e2, slots/clusters (as floats), perm; Z; scratch (G, inverse
+    // iteration's factor: 3 N per cluster); the back-transform's partials
+    const size_t nsplit = (N + kRowChunk - 1) / kRowChunk;
+    return 4 * N + 12 * N + N * N + N + 3 * N * N + nsplit * NBT * N + 2 * (size_t)NBT * N + 2 * (size_t)NBT * NBT +
+           64 * 16;
+}
+
+// Stages 2 and 3 on one matrix after sytrd_one: w_out (n), and if v_out
+// V (n x n) with the eigenvectors as columns; info.
+void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out, uint32_t* info, hipStream_t s) {
+    const int n = (int)nn;
+    const size_t N = nn;
+    float* p = w.rest;
+    auto take = [&](size_t c) {
+        float* r = p;
+        p += (c + 63) / 64 * 64;
+        return r;
+    };
+    float* lam = take(N);
+    float* e2 = take(N);
+    Slot* slots = reinterpret_cast<Slot*>(take(6 * N));
+    Cluster* clusters = reinterpret_cast<Cluster*>(take(4 * N));
+    int* perm = reinterpret_cast<int*>(take(N));
+    float* Z = take(N * N);
+    float* dE = take(N);                 // e with the splits zeroed
+    float* scratch = take(3 * N * N);    // inverse iteration's factor, then Z^T Z
+    const size_t nsplit = (N + kRowChunk - 1) / kRowChunk;
+    float* part = take(nsplit * NBT * N);
+    float* Wb = take((size_t)NBT * N);
+    float* W2 = take((size_t)NBT * N);
+    float* Sg = take((size_t)NBT * NBT);
+    float* Tg = take((size_t)NBT * NBT);
+
+    hipLaunchKernelGGL(set_info_kernel, dim3(1), dim3(1), 0, s, info, w.flags);
+    // the small host-side bookkeeping: T's entries, the splits and Gershgorin
+    // intervals, the clusters and the final order
+    std::vector<float> hd(N), he(N > 1 ? N - 1 : 1);
+    uint32_t hflags[2];
+    MLA_HIP(hipMemcpyAsync(hd.data(), w.d, N * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (n > 1) MLA_HIP(hipMemcpyAsync(he.data(), w.e, (N - 1) * sizeof(float), hipMemcpyDeviceToHost, s));
+    MLA_HIP(hipMemcpyAsync(hflags, w.flags, sizeof(hflags), hipMemcpyDeviceToHost, s));
+    MLA_HIP(hipStreamSynchronize(s));
+    if (hflags[1]) {   // a non-finite entry: all NaN
+        hipLaunchKernelGGL(fill_nan_kernel, dim3(grid_of(N)), dim3(256), 0, s, w_out, N);
+        if (v_out) hipLaunchKernelGGL(fill_nan_kernel, dim3(grid_of(N * N)), dim3(256), 0, s, v_out, N * N);
+        MLA_HIP(hipGetLastError());
+        return;
+    }
+    std::vector<float> he2(N, 0.0f);
+    float tnorm = 0.0f, emax2 = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const float off = (i > 0 ? std::fabs(he[i - 1]) : 0.0f) + (i + 1 < n ? std::fabs(he[i]) : 0.0f);
+        tnorm = std::max(tnorm, std::fabs(hd[i]) + off);
+    }
+    // splits (sstebz): e_i^2 <= eps^2 |d_i d_{i+1}|
+    std::vector<int> bstart;
+    bstart.push_back(0);
+    for (int i = 0; i + 1 < n; ++i) {
+        const float ee = he[i] * he[i];
+        const bool split = ee <= FLT_EPSILON * FLT_EPSILON * std::fabs(hd[i] * hd[i + 1]) || he[i] == 0.0f;
+        he2[i] = split ? 0.0f : ee;
+        if (split) {
+            he[i] = 0.0f;
+            bstart.push_back(i + 1);
+        }
+        emax2 = std::max(emax2, he2[i]);
+    }
+    bstart.push_back(n);
+    const float pivmin = FLT_MIN * std::max(1.0f, emax2);
+    std::vector<Slot> hs(N);
+    for (size_t b = 0; b + 1 < bstart.size(); ++b) {
+        const int s0 = bstart[b], m = bstart[b + 1] - s0;
+        float gl = FLT_MAX, gu = -FLT_MAX;
+        for (int i = s0; i < s0 + m; ++i) {
+            const float off = (i > s0 ? std::fabs(he[i - 1]) : 0.0f) + (i + 1 < s0 + m ? std::fabs(he[i]) : 0.0f);
+            gl = std::min(gl, hd[i] - off);
+            gu = std::max(gu, hd[i] + off);
+        }
+        const float pad = 2.0f * FLT_EPSILON * std::max(std::fabs(gl), std::fabs(gu)) * m + 2.0f * pivmin;
+        for (int k = 0; k < m; ++k) hs[s0 + k] = Slot{s0, m, k, 0, gl - pad, gu + pad};
+    }
+    MLA_HIP(hipMemcpyAsync(e2, he2.data(), N * sizeof(float), hipMemcpyHostToDevice, s));
+    MLA_HIP(hipMemcpyAsync(slots, hs.data(), N * sizeof(Slot), hipMemcpyHostToDevice, s));
+    {
+        KernelTimer tm("tridiag_values", s);
+        hipLaunchKernelGGL(multisection_kernel, dim3((unsigned)cdiv(n, 256 / kMS)), dim3(256), 0, s, w.d, e2, slots,
+                           n, pivmin, lam);
+        tm.stop();
+    }
+    std::vector<float> hl(N);
+    MLA_HIP(hipMemcpyAsync(hl.data(), lam, N * sizeof(float), hipMemcpyDeviceToHost, s));
+    MLA_HIP(hipStreamSynchronize(s));
+    std::vector<int> hp(N);
+    std::iota(hp.begin(), hp.end(), 0);
+    std::stable_sort(hp.begin(), hp.end(), [&](int a, int b) { return hl[a] < hl[b]; });
+    MLA_HIP(hipMemcpyAsync(perm, hp.data(), N * sizeof(int), hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(permute_values_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, lam, w_out, perm, n,
+                       w.flags);
+    if (!v_out) {
+        MLA_HIP(hipStreamSynchronize(s));   // the host vectors above must outlive the copies
+        MLA_HIP(hipGetLastError());
+        return;
+    }
+
+    // clusters: consecutive eigenvalues of a block within 1e-5 ||T||
+    std::vector<Cluster> hc;
+    const float ctol = 1e-5f * tnorm;
+    for (size_t b = 0; b + 1 < bstart.size(); ++b) {
+        const int s0 = bstart[b], m = bstart[b + 1] - s0;
+        int k = 0;
+        while (k < m) {
+            int c = 1;
+            while (k + c < m && hl[s0 + k + c] - hl[s0 + k + c - 1] <= ctol) ++c;
+            hc.push_back(Cluster{s0, m, s0 + k, c});
+            k += c;
+        }
+    }
+    const int ncl = (int)hc.size();
+    MLA_HIP(hipMemcpyAsync(clusters, hc.data(), ncl * sizeof(Cluster), hipMemcpyHostToDevice, s));
+    MLA_HIP(hipMemcpyAsync(dE, he.data(), (N - 1) * sizeof(float), hipMemcpyHostToDevice, s));
+    float* U = scratch;
+    {
+        KernelTimer tm("tridiag_vectors", s);
+        hipLaunchKernelGGL(inverse_iteration_kernel, dim3((unsigned)cdiv(ncl, 256)), dim3(256), 0, s, w.d, dE,
+                           clusters, ncl, lam, tnorm, Z, n, n, U);
+        // Z <- Z (3 I - Z^T Z) / 2
+        float* G = scratch;
+        sgemm(true, false, n, n, n, 1.0f, Z, n, 0, Z, n, 0, 0.0f, G, n, 0, 1, s);
+        hipLaunchKernelGGL(newton_schulz_kernel, dim3((unsigned)cdiv(N * N, 256)), dim3(256), 0, s, G, n);
+        sgemm(false, false, n, n, n, 1.0f, Z, n, 0, G, n, 0, 0.0f, v_out, n, 0, 1, s);
+        MLA_HIP(hipMemcpyAsync(Z, v_out, N * N * sizeof(float), hipMemcpyDeviceToDevice, s));
+        tm.stop();
+    }
+    // V = Q Z: panels from the last, Z2 = Z[j0 + 1 :, :] -= V (T (V^T Z2))
+    {
+        KernelTimer tm("eigh_backtransform", s);
+        const int nrefl = n - 1;
+        for (int j0 = (nrefl - 1) / NBT * NBT; j0 >= 0; j0 -= NBT) {
+            const int nb = std::min(NBT, nrefl - j0);
+            const int rows = n - j0 - 1;
+            const float* Vp = w.V + (size_t)j0 * N + j0 + 1;   // reflector k: Vp[k * N + r], r = row - (j0 + 1)
+            float* Z2 = Z + (size_t)(j0 + 1) * N;
+            // S = V^T V, T
+            split_rows_gemm(true, nb, nb, rows, Vp, n, Vp, n, part, Sg, s);
+            hipLaunchKernelGGL(wy_t_kernel, dim3(1), dim3(64), 0, s, Sg, w.tau + j0, nb, Tg);
+            split_rows_gemm(false, nb, n, rows, Vp, n, Z2, n, part, Wb, s);
+            sgemm(false, false, nb, n, nb, 1.0f, Tg, nb, 0, Wb, n, 0, 0.0f, W2, n, 0, 1, s);
+            sgemm(true, false, rows, n, nb, -1.0f, Vp, n, 0, W2, n, 0, 1.0f, Z2, n, 0, 1, s);
+        }
+        tm.stop();
+    }
+    hipLaunchKernelGGL(permute_columns_kernel, dim3((unsigned)cdiv(N * N, 256)), dim3(256), 0, s, Z, v_out, perm, n);
+    MLA_HIP(hipStreamSynchronize(s));   // the host vectors above must outlive the copies
+    MLA_HIP(hipGetLastError());
+}
+
+}  // namespace mla

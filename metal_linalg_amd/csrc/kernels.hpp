@@ -74,6 +74,10 @@ EighWork eigh_carve(float* base, uint32_t n);
 void sytrd_one(const float* a, uint32_t n, bool lower, const EighWork& w, hipStream_t s);
 // y = x * 2^e (the scale stage 1 took out), or NaN for a non-finite matrix
 void eigh_unscale(const float* x, float* y, uint32_t count, const uint32_t* flags, hipStream_t s);
+// stages 2 and 3 after sytrd_one: eigenvalues (ascending), eigenvectors if
+// v_out, info; the workspace after stage 1's holds eigh_tridiag_floats(n)
+size_t eigh_tridiag_floats(uint32_t n);
+void eigh_tridiag_one(const EighWork& w, uint32_t n, float* w_out, float* v_out, uint32_t* info, hipStream_t s);
 
 // ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128 ----
 bool svd_small_fits(uint32_t m, uint32_t n);

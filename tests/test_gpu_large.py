@@ -292,3 +292,77 @@ def test_sytrd_spectrum(cuda, oracle, n, lower):
     rel = np.abs(np.sort(wt) - wo[0].astype(np.float64)).max() / np.abs(wo[0]).max()
     print(f"[sytrd n={n} lower={lower}] eigenvalues of T vs LAPACK: {rel:.3e}")
     assert rel <= 1e-5
+
+
+def _sym(n, batch, seed, scale=None):
+    rng = np.random.default_rng(seed)
+    g = rng.standard_normal((batch, n, n))
+    s = (g + np.swapaxes(g, -1, -2)) / 2
+    if scale is not None:
+        s *= scale
+    return s.astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [65, 100, 129, 200, 513])
+@pytest.mark.parametrize("lower", [True, False])
+def test_eigh_blocked_shapes(cuda, api, oracle, n, lower):
+    from _util import eigh_residuals, symmetrize, values_close
+
+    a = _sym(n, 2, 1100 + n)
+    junk = a.copy()
+    iu = np.triu_indices(n, 1) if lower else np.tril_indices(n, -1)
+    junk[:, iu[0], iu[1]] = np.nan   # the unread triangle
+    w, v, info = api.eigh(junk, lower, True)
+    wo, vo, io = oracle.eigh(a, lower, True)
+    w, v = to_np(w), to_np(v)
+    assert np.array_equal(u32(info), io)
+    recon, ortho = eigh_residuals(symmetrize(a, lower), w, v)
+    vals = values_close(w, wo)
+    print(f"[eigh n={n} lower={lower}] recon {recon.max():.3e} ortho {ortho.max():.3e} values {vals.max():.3e}")
+    assert recon.max() <= bound(n) and ortho.max() <= bound(n) and vals.max() <= 1e-5
+    wv, _, iv = api.eigh(junk, lower, False)
+    assert values_close(to_np(wv), wo).max() <= 1e-5 and np.array_equal(u32(iv), io)
+
+
+def test_eigh_blocked_special(cuda, api, oracle):
+    from _util import eigh_residuals, values_close
+
+    n = 150
+    a = _sym(n, 6, 31)
+    a[1] = np.nan
+    a[2] = np.diag(np.arange(n, dtype=np.float32) % 7)           # diagonal, repeated values: every e splits
+    a[3] = np.eye(n, dtype=np.float32) * 3.0                      # one value, multiplicity n
+    a[4] = 0.0
+    a[5] *= 1e30                                                   # scaled by a power of two inside
+    w, v, info = api.eigh(a, True, True)
+    wo, vo, io = oracle.eigh(a, True, True)
+    w, v, info = to_np(w), to_np(v), u32(info)
+    assert np.array_equal(info, io)
+    assert np.isnan(w[1]).all() and np.isnan(v[1]).all() and info[1] == 1 << 17
+    ok = [0, 2, 3, 4, 5]
+    recon, ortho = eigh_residuals(a[ok], w[ok], v[ok])
+    vals = values_close(w[ok], wo[ok])
+    print(f"[eigh special] recon {recon} ortho {ortho} values {vals}")
+    assert recon.max() <= bound(n) and ortho.max() <= bound(n) and vals.max() <= 1e-5
+
+
+def test_config5_eigh(cuda, api, oracle):
+    from _util import eigh_residuals, values_close
+
+    torch = cuda
+    g = config5_matrix()
+    a = ((g.astype(np.float64) + g.T) / 2).astype(np.float32)
+    w, v, info = api.eigh(dev(torch, a[None]), True, True)
+    w, v, info = to_np(w), to_np(v), u32(info)
+    # the oracle's path for eigh with vectors (ssyevd); its values-only path
+    # (ssyevd_2stage from n = 128) is itself ~1e-5 off at this size
+    wo, _, io = oracle.eigh(a[None], True, True)
+    recon, ortho = eigh_residuals(a[None], w, v)
+    vals = values_close(w, wo)
+    w64 = np.linalg.eigvalsh(a.astype(np.float64))
+    exact = np.abs(w[0] - w64).max() / np.abs(w64).max()
+    print(f"[eigh config5] recon {recon.max():.3e} ortho {ortho.max():.3e} (bound {bound(4096):.3e}) "
+          f"values vs LAPACK {vals.max():.3e}, vs float64 {exact:.3e}, info {info[0]:#x}")
+    assert recon.max() <= bound(4096) and ortho.max() <= bound(4096) and vals.max() <= 1e-5
+    assert exact <= 1e-6
+    assert info[0] == io[0]
