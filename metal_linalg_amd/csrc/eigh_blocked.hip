@@ -39,8 +39,8 @@ namespace mla {
 namespace {
 
 constexpr int NBT = 64;                        // panel width of the reduction
-constexpr int kColRows = 256;                  // rows per workgroup in sytrd_col
-constexpr int kSymvRows = 16;                  // rows per workgroup in sytrd_symv
+constexpr int kColRows = 64;                   // rows per workgroup in sytrd_col (4 threads per row)
+constexpr int kSymvRows = 16;                  // rows per workgroup in sytrd_symv (16 lanes per row)
 constexpr float kTinySumsq = 8.271806e-25f;    // 2^-80
 
 __device__ __forceinline__ float dpp_row_sum(float v) {
@@ -114,7 +114,7 @@ struct SytrdArgs {
     float* abuf;       // the updated column j (n)
     float* y;          // A22 v of the previous column (n)
     float* partA;      // per-workgroup sums of squares (sytrd_col)
-    float* partB;      // per-workgroup partial dots (sytrd_symv): [wg][2 * NBT + 1]
+    float* partB;      // per-workgroup partial dots (sytrd_symv): [slot][wg], 2 * NBT + 1 slots
     int nwgB;          // workgroups of sytrd_symv
     float* d;
     float* e;
@@ -122,24 +122,82 @@ struct SytrdArgs {
     int update;        // 0: only materialise W[:, i-1] (end of a panel)
 };
 
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+    return v;
+}
+
+// the wave's sum, in every lane
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v = dpp_row_sum(v);
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));   // row_bcast15
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));   // row_bcast31
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// 64 rows per workgroup, 4 threads per row; thread `sub` of a row takes the
+// panel columns k = sub, sub + 4, ...  Every global load of a thread is
+// issued before the first use (clamped addresses), so their latencies
+// overlap.
 __global__ __launch_bounds__(256) void sytrd_col_kernel(SytrdArgs g) {
     __shared__ float q[2 * NBT + 1];   // qV (k < i-1), qW, y^T v of the previous column
     __shared__ float rowj[2 * NBT];    // V[j, k], W[j, k] for k < i
     __shared__ float red[256 / 64];
+    __shared__ float wj;               // W[j, i-1]
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int n = g.n, j = g.j0 + g.i, i = g.i;
-    const int r0 = blockIdx.x * kColRows;
+    const int row = blockIdx.x * kColRows + (t >> 2), sub = t & 3;
+    const int rr = row < n ? row : n - 1;
     const int ip = i - 1;   // the column whose W is materialised
+    // this thread's share of row `row` of V and W (the columns k = sub + 4u)
+    float vk[NBT / 4], wk[NBT / 4];
+#pragma unroll
+    for (int u = 0; u < NBT / 4; ++u) {
+        const int k = sub + 4 * u;
+        const float x = g.Vp[(size_t)(k < i ? k : 0) * n + rr];
+        const float y = g.Wp[(size_t)(k < ip ? k : 0) * n + rr];
+        vk[u] = k < i ? x : 0.0f;
+        wk[u] = k < ip ? y : 0.0f;
+    }
+    const float yr = g.y[rr], vipr = g.Vp[(size_t)(ip >= 0 ? ip : 0) * n + rr];
+    const float arj = g.A[(size_t)rr * n + j];
+    // row j of V and W (W[j, ip] comes from its own dot below)
+    if (g.update && t < i) {
+        rowj[t] = g.Vp[(size_t)t * n + j];
+        rowj[NBT + t] = t < ip ? g.Wp[(size_t)t * n + j] : 0.0f;
+    }
     float tp = 0.0f, alpha2 = 0.0f;
     if (ip >= 0) {
-        // sum the previous column's partial dots: qV[k], qW[k] (k < ip), y^T v
+        // the previous column's partial dots: qV[k], qW[k] (k < ip), y^T v
         const int nv = 2 * ip + 1;
         for (int x = t; x < nv; x += 256) {
             const int slot = x < ip ? x : (x < 2 * ip ? NBT + (x - ip) : 2 * NBT);
-            float s = 0.0f;
-#pragma unroll 8
-            for (int b = 0; b < g.nwgB; ++b) s += g.partB[(size_t)b * (2 * NBT + 1) + slot];
-            q[x] = s;
+            const float* ps = g.partB + (size_t)slot * g.nwgB;
+            float acc = 0.0f;
+            if ((g.nwgB & 3) == 0) {
+                for (int b0 = 0; b0 < g.nwgB; b0 += 128) {
+                    float4 pv[32];
+#pragma unroll
+                    for (int u = 0; u < 32; ++u) {
+                        const int b = b0 + 4 * u;
+                        pv[u] = *reinterpret_cast<const float4*>(ps + (b < g.nwgB ? b : 0));
+                    }
+                    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int u = 0; u < 32; ++u)
+                        if (b0 + 4 * u < g.nwgB) {
+                            s4[0] += pv[u].x;
+                            s4[1] += pv[u].y;
+                            s4[2] += pv[u].z;
+                            s4[3] += pv[u].w;
+                        }
+                    acc += (s4[0] + s4[1]) + (s4[2] + s4[3]);
+                }
+            } else {
+                for (int b = 0; b < g.nwgB; ++b) acc += ps[b];
+            }
+            q[x] = acc;
         }
         __syncthreads();
         tp = g.tau[g.j0 + ip];
@@ -148,111 +206,165 @@ __global__ __launch_bounds__(256) void sytrd_col_kernel(SytrdArgs g) {
         for (int k = 0; k < ip; ++k) qq = fmaf(q[k], q[ip + k], qq);
         alpha2 = -0.5f * tp * (tp * (q[2 * ip] - 2.0f * qq));
     }
-    // W[:, ip] for this block's rows (defined on rows >= j), and row j of V, W
-    const float* vp = g.Vp + (size_t)ip * n;
-    auto wval = [&](int r) {
-        float s = g.y[r];
-#pragma unroll 4
-        for (int k = 0; k < ip; ++k) s = fmaf(-g.Wp[(size_t)k * n + r], q[k], fmaf(-g.Vp[(size_t)k * n + r], q[ip + k], s));
-        return fmaf(tp, s, alpha2 * vp[r]);
-    };
+    // W[row, ip] = tau (y - W qV - V qW) + alpha' v  (rows >= j)
+    float wnew = 0.0f;
     if (ip >= 0) {
-        for (int r = r0 + t; r < min(n, r0 + kColRows); r += 256)
-            g.Wp[(size_t)ip * n + r] = r >= j ? wval(r) : 0.0f;
+        float sp = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NBT / 4; ++u) {
+            const int k = sub + 4 * u;
+            if (k < ip) sp = fmaf(wk[u], q[k], fmaf(vk[u], q[ip + k], sp));
+        }
+        sp = quad_sum(sp);
+        wnew = row >= j ? fmaf(tp, yr - sp, alpha2 * vipr) : 0.0f;
+        if (sub == 0 && row < n) g.Wp[(size_t)ip * n + row] = wnew;
     }
     if (!g.update) return;
-    for (int k = t; k < i; k += 256) {
-        rowj[k] = g.Vp[(size_t)k * n + j];
-        rowj[NBT + k] = k == ip ? wval(j) : g.Wp[(size_t)k * n + j];
+    __syncthreads();   // rowj
+    if (t == 0) {
+        float wv0 = 0.0f;
+        if (ip >= 0) {
+            float sp = 0.0f;
+            for (int k = 0; k < ip; ++k) sp = fmaf(rowj[NBT + k], q[k], fmaf(rowj[k], q[ip + k], sp));
+            wv0 = fmaf(tp, g.y[j] - sp, alpha2 * rowj[ip]);
+        }
+        wj = wv0;
     }
     __syncthreads();
-    // a = A[:, j] - V W[j, :]^T - W V[j, :]^T on rows >= j; partial tail sums of squares
-    float ss = 0.0f;
-    for (int r = r0 + t; r < min(n, r0 + kColRows); r += 256) {
-        if (r < j) continue;
-        float s = g.A[(size_t)r * n + j];
-        // (W[:, ip] of this row was written just above by this thread)
-#pragma unroll 4
-        for (int k = 0; k < i; ++k)
-            s = fmaf(-g.Vp[(size_t)k * n + r], rowj[NBT + k], fmaf(-g.Wp[(size_t)k * n + r], rowj[k], s));
-        g.abuf[r] = s;
-        if (r == j) g.d[j] = s;
-        if (r >= j + 2) ss = fmaf(s, s, ss);
+    // a = A[:, j] - V W[j, :]^T - W V[j, :]^T on rows >= j
+    float sa = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NBT / 4; ++u) {
+        const int k = sub + 4 * u;
+        if (k < i) {
+            const float wkk = k == ip ? wnew : wk[u];
+            const float wjk = k == ip ? wj : rowj[NBT + k];
+            sa = fmaf(vk[u], wjk, fmaf(wkk, rowj[k], sa));
+        }
     }
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    sa = quad_sum(sa);
+    const float av = arj - sa;
+    float ss = 0.0f;
+    if (sub == 0 && row < n && row >= j) {
+        g.abuf[row] = av;
+        if (row == j) g.d[j] = av;
+        if (row >= j + 2) ss = av * av;
+    }
+    ss = wave_sum_f(ss);
     if (lane == 0) red[wv] = ss;
     __syncthreads();
-    if (t == 0) g.partA[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+    if (t == 0) g.partA[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// 16 rows per workgroup: the reflector (every workgroup forms all of v in
+// LDS), y = A22 v, and the partial dot products for the next column.
 __global__ __launch_bounds__(256) void sytrd_symv_kernel(SytrdArgs g, int nwgA) {
     extern __shared__ float v[];   // the reflector, whole (n floats)
-    __shared__ float sc[4];
+    __shared__ float sc[2];
     __shared__ float yrow[kSymvRows];
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int n = g.n, j = g.j0 + g.i, i = g.i;
-    if (t == 0) {
+    if (wv == 0) {
         float ss = 0.0f;
-        for (int b = 0; b < nwgA; ++b) ss += g.partA[b];
-        const float alpha = j + 1 < n ? g.abuf[j + 1] : 0.0f;
-        float beta = alpha, tau = 0.0f, scal = 1.0f;
-        if (ss >= kTinySumsq) {
-            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-            tau = (beta - alpha) / beta;
-            scal = 1.0f / (alpha - beta);
-        }
-        sc[0] = tau;
-        sc[1] = scal;
-        if (blockIdx.x == 0) {
-            g.e[j] = beta;
-            g.tau[j] = tau;
+        for (int b = lane; b < nwgA; b += 64) ss += g.partA[b];
+        ss = wave_sum_f(ss);
+        if (lane == 0) {
+            const float alpha = j + 1 < n ? g.abuf[j + 1] : 0.0f;
+            float beta = alpha, tau = 0.0f, scal = 1.0f;
+            if (ss >= kTinySumsq) {
+                beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
+                tau = (beta - alpha) / beta;
+                scal = 1.0f / (alpha - beta);
+            }
+            sc[0] = tau;
+            sc[1] = scal;
+            if (blockIdx.x == 0) {
+                g.e[j] = beta;
+                g.tau[j] = tau;
+            }
         }
     }
     __syncthreads();
     const float scal = sc[1];
-    for (int r = t; r < n; r += 256) v[r] = r < j + 1 ? 0.0f : (r == j + 1 ? 1.0f : g.abuf[r] * scal);
-    __syncthreads();
-    const int r0 = blockIdx.x * kSymvRows;
-    for (int r = r0 + t; r < min(n, r0 + kSymvRows); r += 256) g.Vp[(size_t)i * n + r] = v[r];
-    // y = A22 v for rows r0 .. r0 + 15 (16 lanes per row, float4 columns from
-    // the aligned column at or before j + 1; v is zero left of j + 1)
-    const int row = r0 + (t >> 4), sub = t & 15;
-    const int c0 = (j + 1) & ~3;
-    float acc = 0.0f;
-    if (row < n && row >= j + 1) {
-        const float* ar = g.A + (size_t)row * n;
-        if ((n & 3) == 0) {
-            for (int c = c0 + sub * 4; c < n; c += 64) {
-                const float4 x = *reinterpret_cast<const float4*>(ar + c);
-                acc = fmaf(x.x, v[c], fmaf(x.y, v[c + 1], fmaf(x.z, v[c + 2], fmaf(x.w, v[c + 3], acc))));
-            }
-        } else {
-            for (int c = j + 1 + sub; c < n; c += 16) acc = fmaf(ar[c], v[c], acc);
+    // v from the updated column (16 loads in flight per round)
+    for (int r0 = 0; r0 < n; r0 += 256 * 16) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int r = r0 + t + 256 * u;
+            x[u] = g.abuf[r < n ? r : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int r = r0 + t + 256 * u;
+            if (r < n) v[r] = r < j + 1 ? 0.0f : (r == j + 1 ? 1.0f : x[u] * scal);
         }
     }
-    acc = dpp_row_sum(acc);
-    if (sub == 0 && row < n) {
-        const float yr = row >= j + 1 ? acc : 0.0f;
-        g.y[row] = yr;
-        yrow[t >> 4] = yr;
+    __syncthreads();
+    const int rb = blockIdx.x * kSymvRows;
+    for (int r = rb + t; r < min(n, rb + kSymvRows); r += 256) g.Vp[(size_t)i * n + r] = v[r];
+    // y = A22 v: 16 lanes per row; a row's columns as float4s from the
+    // aligned column at or before j + 1 (v is zero left of j + 1), 16 loads
+    // in flight per lane
+    const int c0 = (j + 1) & ~3;
+    const bool vec = (n & 3) == 0;
+    const int sub = t & 15;
+    {
+        const int row = rb + (t >> 4);
+        float acc = 0.0f;
+        if (row < n && row >= j + 1) {
+            const float* ar = g.A + (size_t)row * n;
+            if (vec) {
+                for (int cb = c0 + sub * 4; cb < n; cb += 64 * 16) {
+                    float4 xs[16];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        const int c = cb + 64 * u;
+                        xs[u] = *reinterpret_cast<const float4*>(ar + (c < n ? c : c0));
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        const int c = cb + 64 * u;
+                        if (c < n)
+                            acc = fmaf(xs[u].x, v[c],
+                                       fmaf(xs[u].y, v[c + 1], fmaf(xs[u].z, v[c + 2], fmaf(xs[u].w, v[c + 3], acc))));
+                    }
+                }
+            } else {
+                for (int c = j + 1 + sub; c < n; c += 16) acc = fmaf(ar[c], v[c], acc);
+            }
+        }
+        acc = dpp_row_sum(acc);
+        if (sub == 0 && row < n) {
+            const float yv = row >= j + 1 ? acc : 0.0f;
+            g.y[row] = yv;
+            yrow[t >> 4] = yv;
+        }
     }
     __syncthreads();
-    // partial dots over this block's rows: V_k^T v, W_k^T v (k < i), y^T v
-    float* out = g.partB + (size_t)blockIdx.x * (2 * NBT + 1);
+    // partial dots over this block's rows: V_k^T v, W_k^T v (k < i), y^T v;
+    // a thread per value, its 64 rows as float4s
+    const int nwg = gridDim.x;
     for (int x = t; x < 2 * i + 1; x += 256) {
         const float* src = x < i ? g.Vp + (size_t)x * n : (x < 2 * i ? g.Wp + (size_t)(x - i) * n : nullptr);
-        float o[kSymvRows];
-#pragma unroll
-        for (int rr = 0; rr < kSymvRows; ++rr) {
-            const int r = min(r0 + rr, n - 1);
-            o[rr] = src ? src[r] : yrow[rr];
-        }
         float s = 0.0f;
+        if (src && vec && rb + kSymvRows <= n) {
+            float4 o[kSymvRows / 4];
 #pragma unroll
-        for (int rr = 0; rr < kSymvRows; ++rr)
-            if (r0 + rr < n) s = fmaf(o[rr], v[r0 + rr], s);
+            for (int u = 0; u < kSymvRows / 4; ++u) o[u] = *reinterpret_cast<const float4*>(src + rb + 4 * u);
+#pragma unroll
+            for (int u = 0; u < kSymvRows / 4; ++u) {
+                const int r = rb + 4 * u;
+                s = fmaf(o[u].x, v[r], fmaf(o[u].y, v[r + 1], fmaf(o[u].z, v[r + 2], fmaf(o[u].w, v[r + 3], s))));
+            }
+        } else {
+            for (int rr = 0; rr < kSymvRows; ++rr) {
+                const int r = rb + rr;
+                if (r < n) s = fmaf(src ? src[r] : yrow[rr], v[r], s);
+            }
+        }
         const int slot = x < i ? x : (x < 2 * i ? NBT + (x - i) : 2 * NBT);
-        out[slot] = s;
+        g.partB[(size_t)slot * nwg + blockIdx.x] = s;
     }
 }
 

@@ -12,7 +12,7 @@
 //   - eigenvalues by multisection of the Sturm count: 16 lanes per
 //     eigenvalue evaluate 16 points at once, so an iteration narrows the
 //     interval 17-fold (sstebz bisects);
-//   - eigenvectors by inverse iteration from a pseudo-random start, three
+//   - eigenvectors by inverse iteration from a pseudo-random start, two
 //     solves with (T - lambda I) factored with partial pivoting (slagtf /
 //     slagts), one thread per cluster of eigenvalues closer than
 //     1e-5 ||T||, modified Gram-Schmidt inside a cluster (sstein);
@@ -37,7 +37,8 @@ namespace {
 
 constexpr int NBT = 64;        // the reduction's panel width (reflectors per block)
 constexpr int kMS = 16;        // multisection points per eigenvalue
-constexpr int kIters = 3;      // inverse-iteration solves
+constexpr int kIters = 2;      // inverse-iteration solves
+constexpr int CH = 16;         // rows per chunk of the inverse iteration's passes
 
 struct Slot {            // one eigenvalue: its block and its place in it
     int start, size, local, pad;
@@ -134,46 +135,62 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
         const float lambda = lam[slot];
         for (int r = 0; r < m; ++r) z[(size_t)(s + r) * ldz] = hash_uniform((unsigned)slot, (unsigned)r);
         for (int it = 0; it < kIters; ++it) {
-            // forward: factor (T - lambda I) = P L U on the fly, apply P, L to z
+            // forward: factor (T - lambda I) = P L U on the fly, apply P, L to
+            // z.  Rows move in chunks of CH: all of a chunk's loads are issued
+            // before its recurrence runs.
             float a = d[s] - lambda;         // the running diagonal entry of row k
             float cc = e[s];                 // row k's superdiagonal
             float b0 = z[(size_t)s * ldz];   // the running right-hand side of row k
-            for (int k = 0; k < m - 1; ++k) {
-                const float bk = e[s + k];           // subdiagonal (row k + 1, column k)
-                const float an = d[s + k + 1] - lambda;
-                const float cn = k + 1 < m - 1 ? e[s + k + 1] : 0.0f;
-                const float b1 = z[(size_t)(s + k + 1) * ldz];
-                float p0, p1, p2, nb0, na, nc, rhs;
-                if (fabsf(a) >= fabsf(bk)) {
-                    const float l = a == 0.0f ? 0.0f : bk / a;
-                    p0 = a;
-                    p1 = cc;
-                    p2 = 0.0f;
-                    rhs = b0;
-                    na = an - l * cc;
-                    nc = cn;
-                    nb0 = b1 - l * b0;
-                } else {
-                    const float l = a / bk;
-                    p0 = bk;
-                    p1 = an;
-                    p2 = cn;
-                    rhs = b1;
-                    na = cc - l * an;
-                    nc = -l * cn;
-                    nb0 = b0 - l * b1;
+            for (int k0 = 0; k0 < m - 1; k0 += CH) {
+                float zb[CH], db[CH], eb[CH], en[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int k = min(k0 + c, m - 2);
+                    zb[c] = z[(size_t)(s + k + 1) * ldz];
+                    db[c] = d[s + k + 1];
+                    eb[c] = e[s + k];
+                    en[c] = k + 1 < m - 1 ? e[s + k + 1] : 0.0f;
                 }
-                if (p0 == 0.0f) p0 = tol;
-                u0[(3 * (size_t)k + 0) * us] = p0;
-                u0[(3 * (size_t)k + 1) * us] = p1;
-                u0[(3 * (size_t)k + 2) * us] = p2;
-                z[(size_t)(s + k) * ldz] = rhs;
-                a = na;
-                cc = nc;
-                b0 = nb0;
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int k = k0 + c;
+                    if (k >= m - 1) break;
+                    const float bk = eb[c];
+                    const float an = db[c] - lambda;
+                    const float cn = en[c];
+                    const float b1 = zb[c];
+                    float p0, p1, p2, nb0, na, nc, rhs;
+                    if (fabsf(a) >= fabsf(bk)) {
+                        const float l = a == 0.0f ? 0.0f : bk * __builtin_amdgcn_rcpf(a);
+                        p0 = a;
+                        p1 = cc;
+                        p2 = 0.0f;
+                        rhs = b0;
+                        na = an - l * cc;
+                        nc = cn;
+                        nb0 = b1 - l * b0;
+                    } else {
+                        const float l = a * __builtin_amdgcn_rcpf(bk);
+                        p0 = bk;
+                        p1 = an;
+                        p2 = cn;
+                        rhs = b1;
+                        na = cc - l * an;
+                        nc = -l * cn;
+                        nb0 = b0 - l * b1;
+                    }
+                    if (p0 == 0.0f) p0 = tol;
+                    u0[(3 * (size_t)k + 0) * us] = __builtin_amdgcn_rcpf(p0);   // the backward pass multiplies
+                    u0[(3 * (size_t)k + 1) * us] = p1;
+                    u0[(3 * (size_t)k + 2) * us] = p2;
+                    z[(size_t)(s + k) * ldz] = rhs;
+                    a = na;
+                    cc = nc;
+                    b0 = nb0;
+                }
             }
             if (a == 0.0f) a = tol;
-            // backward: U x = rhs, and |x|^2
+            // backward: U x = rhs, and |x|^2, in chunks from the bottom
             float x2 = 0.0f, x1 = 0.0f, nrm = 0.0f;
             {
                 const float x = b0 / a;
@@ -181,15 +198,26 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
                 x1 = x;
                 nrm = x * x;
             }
-            for (int k = m - 2; k >= 0; --k) {
-                const float p0 = u0[(3 * (size_t)k + 0) * us];
-                const float p1 = u0[(3 * (size_t)k + 1) * us];
-                const float p2 = u0[(3 * (size_t)k + 2) * us];
-                const float x = (z[(size_t)(s + k) * ldz] - p1 * x1 - p2 * x2) / p0;
-                z[(size_t)(s + k) * ldz] = x;
-                x2 = x1;
-                x1 = x;
-                nrm = fmaf(x, x, nrm);
+            for (int k1 = m - 2; k1 >= 0; k1 -= CH) {
+                float r0[CH], r1[CH], r2[CH], rz[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int k = max(k1 - c, 0);
+                    r0[c] = u0[(3 * (size_t)k + 0) * us];
+                    r1[c] = u0[(3 * (size_t)k + 1) * us];
+                    r2[c] = u0[(3 * (size_t)k + 2) * us];
+                    rz[c] = z[(size_t)(s + k) * ldz];
+                }
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int k = k1 - c;
+                    if (k < 0) break;
+                    const float x = (rz[c] - r1[c] * x1 - r2[c] * x2) * r0[c];
+                    z[(size_t)(s + k) * ldz] = x;
+                    x2 = x1;
+                    x1 = x;
+                    nrm = fmaf(x, x, nrm);
+                }
             }
             // against the cluster's earlier vectors (modified Gram-Schmidt)
             for (int p = 0; p < q; ++p) {
@@ -204,7 +232,14 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
                 }
             }
             const float inv = nrm > 0.0f ? 1.0f / sqrtf(nrm) : 0.0f;
-            for (int r = 0; r < m; ++r) z[(size_t)(s + r) * ldz] *= inv;
+            for (int r0 = 0; r0 < m; r0 += CH) {
+                float x[CH];
+#pragma unroll
+                for (int c = 0; c < CH; ++c) x[c] = z[(size_t)(s + min(r0 + c, m - 1)) * ldz];
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+                    if (r0 + c < m) z[(size_t)(s + r0 + c) * ldz] = x[c] * inv;
+            }
         }
     }
 }
@@ -225,10 +260,20 @@ __global__ __launch_bounds__(64) void wy_t_kernel(const float* __restrict__ S, c
     __shared__ float Ts[NBT][NBT + 1];
     __shared__ float Ss[NBT][NBT + 1];
     const int t = threadIdx.x;
-    for (int idx = t; idx < NBT * NBT; idx += 64) {
-        const int i = idx / NBT, j = idx % NBT;
-        Ss[i][j] = (i < nb && j < nb) ? S[i * nb + j] : 0.0f;
-        Ts[i][j] = 0.0f;
+    for (int i0 = 0; i0 < NBT; i0 += 16) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = i0 + u;
+            const bool in = i < nb && t < nb;
+            x[u] = S[in ? i * nb + t : 0];
+            x[u] = in ? x[u] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            Ss[i0 + u][t] = x[u];
+            Ts[i0 + u][t] = 0.0f;
+        }
     }
     __syncthreads();
     for (int k = 0; k < nb; ++k) {
@@ -445,9 +490,11 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
         const int nrefl = n - 1;
         for (int j0 = (nrefl - 1) / NBT * NBT; j0 >= 0; j0 -= NBT) {
             const int nb = std::min(NBT, nrefl - j0);
-            const int rows = n - j0 - 1;
-            const float* Vp = w.V + (size_t)j0 * N + j0 + 1;   // reflector k: Vp[k * N + r], r = row - (j0 + 1)
-            float* Z2 = Z + (size_t)(j0 + 1) * N;
+            // rows j0 .. n-1 (row j0 is zero in every reflector of the panel,
+            // kept so that the operands stay 16-byte aligned)
+            const int rows = n - j0;
+            const float* Vp = w.V + (size_t)j0 * N + j0;   // reflector k: Vp[k * N + r], r = row - j0
+            float* Z2 = Z + (size_t)j0 * N;
             // S = V^T V, T
             split_rows_gemm(true, nb, nb, rows, Vp, n, Vp, n, part, Sg, s);
             hipLaunchKernelGGL(wy_t_kernel, dim3(1), dim3(64), 0, s, Sg, w.tau + j0, nb, Tg);
