@@ -67,16 +67,12 @@ class Workload:
         return self.batch * calls / seconds
 
 
-def blocked_lu_gemm_flops(n, nb=128, w=16):
-    """Flops of the blocked LU's matrix-core updates: inside each panel the
-    leaf updates (rows below the leaf x the panel's later columns x w), and
-    per panel the trailing A22 -= L21 U12."""
+def blocked_lu_gemm_flops(n, nb=128):
+    """Flops of the blocked LU's matrix-core updates: per panel the trailing
+    A22 -= L21 U12 (the in-panel updates are thin VALU kernels)."""
     f = 0
     for pj in range(0, n, nb):
         pe = min(pj + nb, n)
-        for pc in range(pj, pe, w):
-            ww = min(w, pe - pc)
-            f += 2 * (n - pc - ww) * (pe - pc - ww) * ww
         nc = n - pe
         f += 2 * nc * nc * (pe - pj)
     return f
