@@ -49,6 +49,19 @@ __device__ __forceinline__ int scale_exponent(float amax) {
     return e;
 }
 
+// A reproducible pseudo-random value in (-1, 1) from two integers (an
+// integer hash: xor-shift-multiply rounds).  Start vectors of inverse
+// iteration.
+__device__ __forceinline__ float hash_uniform(unsigned a, unsigned b) {
+    unsigned x = a * 0x9E3779B1u ^ (b + 0x7F4A7C15u) * 0x85EBCA77u;
+    x ^= x >> 15;
+    x *= 0x2C1B3C6Du;
+    x ^= x >> 12;
+    x *= 0x297A2D39u;
+    x ^= x >> 15;
+    return (float)(x >> 8) * (2.0f / 16777216.0f) - 1.0f;
+}
+
 // A wave-level fence for LDS traffic between lanes of one wavefront: the
 // kernels that use it launch one wave per workgroup.
 __device__ __forceinline__ void wave_lds_sync() { __syncthreads(); }

@@ -2,29 +2,33 @@
 // matrix per lane group of a wave64 (a whole wave at n = 64), in registers.
 //
 // Role: the MI355X counterpart of the reference's eigh_ql kernel
-// (reference: shaders/Eigh_QL.metal:229-485, driver src/eigh_ql.mm:169-266),
-// LAPACK's method per matrix: Householder tridiagonalisation (ssytd2),
-// the orthogonal factor, implicit QL iterations with a Wilkinson-type shift
-// on the tridiagonal (the method of EISPACK tql2 / LAPACK ssteqr) with the
-// rotations applied to the eigenvectors, and an ascending sort.  Conventions
-// of the reference's contract: only the requested triangle is read; the
-// matrix is scaled by a power of two into [0.5, 1) before and the values
-// unscaled after; a matrix holding a NaN or an infinity in the read triangle
-// gives all-NaN w and V with info bit 17; info otherwise counts the QL
-// iterations in bits 0-15 with bit 16 set once every eigenvalue converged
-// (at most 30 n iterations, ssteqr's budget).
+// (reference: shaders/Eigh_QL.metal:229-485, driver src/eigh_ql.mm:169-266).
+// Same contract, different method for the tridiagonal stage: Householder
+// tridiagonalisation (LAPACK ssytd2), then every eigenvalue by bisection on
+// Sturm counts (LAPACK sstebz's rule) and every eigenvector by inverse
+// iteration with partial pivoting (LAPACK slagtf/slagts, as in sstein), two
+// steps from a pseudo-random start, with modified Gram-Schmidt inside groups
+// of eigenvalues closer than 1e-3 |T| (sstein's ORTOL), and finally the
+// back-transformation by the reflectors.  Conventions of the reference's
+// contract: only the requested triangle is read; the matrix is scaled by a
+// power of two into [0.5, 1) before and the values unscaled after; a matrix
+// holding a NaN or an infinity in the read triangle gives all-NaN w and V
+// with info bit 17; otherwise info holds the number of bisection steps in
+// bits 0-15 with bit 16 (converged) set; values ascending.
 //
 // MI355X layout: lane c of an N-lane group owns column c of the (symmetric)
 // working matrix, so the tridiagonalisation's products A v are lane-local
-// FMA chains and only v and w are broadcast through LDS.  The orthogonal
-// factor is accumulated as Q^T = H_{n-3} ... H_0 in the same layout, which
-// leaves lane r holding row r of Q: a QL rotation of columns (i, i+1) is
-// then two registers of every lane.  The QL recurrence runs redundantly on
-// every lane of the group with d and e in registers (the sweep loop is
-// unrolled so every index is compile-time; inactive positions are skipped
-// by a group-uniform branch), mirrored in LDS for the split search, which
-// the group's lanes do in parallel (one candidate position each, then a
-// ballot).
+// FMA chains and only v and w are broadcast through LDS.  The tridiagonal
+// stage is lane-parallel: lane c bisects for the c-th smallest eigenvalue
+// (each Sturm count a register-resident recurrence over d and e^2 read from
+// LDS as float4 broadcasts), then solves for its own eigenvector with the
+// pivoted factor, right-hand side and back substitution in VGPRs.  Lanes of
+// a close group exchange vectors with cross-lane permutes, one member per
+// round.  Lane c then applies the reflectors to its vector and writes column
+// c of V; lanes write consecutive addresses.  The previous design ran
+// implicit QL on every lane redundantly: a serial rotation chain that kept
+// 63 of 64 lanes idle (the bisection and the solves need ~30x fewer issue
+// slots per matrix).
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "runtime.hpp"
@@ -36,14 +40,19 @@ constexpr float kEps = 5.9604645e-08f;        // 2^-24, fp32 unit roundoff
 constexpr float kTinySumsq = 8.271806e-25f;   // 2^-80: a reflector below it is the identity
 constexpr float kSafeMin = 1.17549435e-38f;   // FLT_MIN
 
+constexpr float kPad = 0x1p100f;             // the diagonal of padding rows: never counted
+constexpr float kOrtol = 1e-3f;               // close eigenvalues: gap <= kOrtol |T| (sstein's ORTOL)
+constexpr int kMaxBisect = 64;
+
 template <int N>
-struct EighLds {
+struct alignas(16) EighLds {
     float vs[N][N + 1];   // staging of the read triangle, then the reflectors v_k (row k)
     float bc[N + 4];      // per-step broadcast (v, then w)
-    float d[N + 1];
-    float e[N + 1];
+    float d[N + 4];       // the tridiagonal, rows >= n padded with kPad
+    float e[N + 4];       // e[k] couples rows k and k+1; zero at splits and from row n - 1 on
+    float f[N + 4];       // f[k] = e[k-1]^2, f[0] = 0
+    float re[N + 4];      // 1 / e[k] (0 where e[k] = 0)
     float tau[N];
-    int perm[N];
 };
 
 // sum of x[r] * y[r] over r in [LO, N), four partial sums
@@ -91,7 +100,11 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
             float v[N];
 #pragma unroll
             for (int r = K + 1; r < N; ++r) v[r] = s.bc[r];
-            const bool act = c > K && c < n;
+            // c laundered: otherwise the compiler precomputes this lane mask
+            // for every step at kernel entry and spills the SGPR pairs
+            int cl = c;
+            __asm__ volatile("" : "+v"(cl));
+            const bool act = cl > K && cl < n;
             float p = 0.0f, vc = 0.0f;
             if (act) {
                 vc = s.bc[c];
@@ -112,10 +125,53 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
     }
 }
 
-// Q^T <- H_K Q^T (forward accumulation; lane r holds column r of Q^T).
+// Number of eigenvalues of the (split) tridiagonal below x: the LDL^T
+// recurrence of T - x I with tiny pivots replaced by -pivmin (LAPACK
+// slaebz's count).  d and f = e^2 (shifted by one row) are read four rows at
+// a time from LDS; rows past n carry kPad and count nothing.
+template <int N>
+__device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float pivmin) {
+    int cnt = 0;
+    float t = 1.0f;
+#pragma unroll
+    for (int k0 = 0; k0 < N; k0 += 4) {
+        const float4 dv = *reinterpret_cast<const float4*>(&s.d[k0]);
+        const float4 fv = *reinterpret_cast<const float4*>(&s.f[k0]);
+        const float dk[4] = {dv.x, dv.y, dv.z, dv.w};
+        const float fk[4] = {fv.x, fv.y, fv.z, fv.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            t = fmaf(-fk[j], __builtin_amdgcn_rcpf(t), dk[j] - x);
+            t = fabsf(t) < pivmin ? -pivmin : t;
+            cnt += (int)(__float_as_uint(t) >> 31);
+        }
+    }
+    return cnt;
+}
+
+// x <- x / |x|_2, scaled by its largest entry first.
+template <int N>
+__device__ __forceinline__ void normalize(float (&x)[N]) {
+    float xm = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) xm = fmaxf(xm, fabsf(x[k]));
+    const float sc = xm > 0.0f ? 1.0f / xm : 0.0f;
+    float nrm = 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        x[k] *= sc;
+        nrm = fmaf(x[k], x[k], nrm);
+    }
+    const float inv = nrm > 0.0f ? 1.0f / sqrtf(nrm) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < N; ++k) x[k] *= inv;
+}
+
+// x <- H_K x for K = K0, K0-1, ..., 0: the eigenvector of T in lane c
+// becomes that of A (Q = H_0 H_1 ... H_{n-3}).
 template <int K, int N>
-__device__ __forceinline__ void accumulate_step(float (&x)[N], EighLds<N>& s, int n) {
-    if constexpr (K + 2 < N) {
+__device__ __forceinline__ void backtransform_step(float (&x)[N], const EighLds<N>& s, int n) {
+    if constexpr (K >= 0) {
         if (K + 2 < n) {
             const float tau = s.tau[K];
             float v[N];
@@ -125,7 +181,7 @@ __device__ __forceinline__ void accumulate_step(float (&x)[N], EighLds<N>& s, in
 #pragma unroll
             for (int r = K + 1; r < N; ++r) x[r] = fmaf(-d, v[r], x[r]);
         }
-        accumulate_step<K + 1, N>(x, s, n);
+        backtransform_step<K - 1, N>(x, s, n);
     }
 }
 
@@ -201,131 +257,168 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     }
     wave_lds_sync();
 
-    // 3. Q^T = H_{n-3} ... H_0 I, lane r ends holding row r of Q
-    if (VEC) {
+    // 3. splits (sstebz's test, as ssteqr's), e^2, padding, Gershgorin bounds
+    float ei = 0.0f;
+    if (c < nn - 1) {
+        ei = s.e[c];
+        const float di = s.d[c], di1 = s.d[c + 1];
+        if (fabsf(ei) <= kEps * (fabsf(di) + fabsf(di1)) || fabsf(ei) < kSafeMin) ei = 0.0f;
+    }
+    const bool split = c < nn - 1 && ei == 0.0f;
+    uint64_t splits = __ballot(split);
+    if (N < 64) splits = (splits >> (g * N)) & ((1ull << N) - 1);
+    s.e[c] = ei;               // zero from row n - 1 on
+    s.f[c + 1] = ei * ei;
+    s.re[c] = ei != 0.0f ? __builtin_amdgcn_rcpf(ei) : 0.0f;
+    if (c == 0) s.f[0] = 0.0f;
+    if (c >= nn) s.d[c] = kPad;
+    if (c < 4) {
+        s.d[N + c] = kPad;
+        s.e[N + c] = 0.0f;
+        if (c > 0) s.f[N + c] = 0.0f;
+        s.re[N + c] = 0.0f;
+    }
+    wave_lds_sync();
+    float glo = FLT_MAX, ghi = -FLT_MAX;
+    if (c < nn) {
+        const float r = fabsf(ei) + (c > 0 ? fabsf(s.e[c - 1]) : 0.0f);
+        const float dc = s.d[c];
+        glo = dc - r;
+        ghi = dc + r;
+    }
+    glo = -group_max<N>(-glo);
+    ghi = group_max<N>(ghi);
+    const float e2max = group_max<N>(ei * ei);
+    const float tnorm = fmaxf(fabsf(glo), fabsf(ghi));
+    const float pivmin = kSafeMin * fmaxf(1.0f, e2max);
+    const float slack = 2.1f * 2.0f * kEps * tnorm * (float)nn + 4.2f * pivmin;
+    const float atol = fmaxf(kEps * tnorm, 2.0f * pivmin);
+
+    // 4. bisection: lane c brackets the c-th smallest eigenvalue
+    const bool mine = c < nn;
+    float lo = glo - slack, hi = ghi + slack;
+    int steps = 0;
+    while (steps < kMaxBisect) {
+        const float mid = 0.5f * (lo + hi);
+        const int cm = sturm_count<N>(s, mid, pivmin);
+        if (cm > c) {
+            hi = mid;
+        } else {
+            lo = mid;
+        }
+        ++steps;
+        const bool done = !mine || hi - lo <= fmaxf(atol, 2.0f * kEps * fmaxf(fabsf(lo), fabsf(hi)));
+        if (__ballot(!done) == 0) break;
+    }
+    // ascending even where brackets of equal eigenvalues overlap: prefix max
+    float lam = 0.5f * (lo + hi);
 #pragma unroll
-        for (int r = 0; r < N; ++r) x[r] = r == c ? 1.0f : 0.0f;
-        accumulate_step<0, N>(x, s, nn);
+    for (int off = 1; off < N; off <<= 1) {
+        const float up = __shfl_up(lam, off, N);
+        if (c >= off) lam = fmaxf(lam, up);
     }
 
-    // 4. implicit QL on (d, e), rotations applied to the rows of Q
-    float dd[N], ee[N];
+    if (VEC) {
+        // 5. inverse iteration: T - lam I = P L U with partial pivoting
+        // (slagtf), the right-hand side carried along.  x[k] holds the
+        // right-hand side, then row k of U scaled by its pivot (x, and u =
+        // the superdiagonal entry where row k kept its place), then the
+        // solution.  Where rows k and k+1 were swapped (bit k of sw), U's row
+        // is (e_k, d_{k+1} - lam, e_{k+1}), rebuilt from LDS on the way back.
+        // The whole tridiagonal is solved: at a split (e = 0) the
+        // elimination decouples, and rows past n (kPad, e = 0) carry zeros.
+        // Eigenvectors of other blocks with an eigenvalue as close as this
+        // one's fall into its close group below.
+        const float tol = fmaxf(kEps * tnorm, kSafeMin);   // smaller pivots become +-tol
+        float u[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-        dd[i] = s.d[i];
-        ee[i] = s.e[i];
-    }
-    int iters = 0;
-    bool converged = true;
-    const int budget = 30 * nn;
-    for (int l = 0; l < nn && converged; ++l) {
-        while (true) {
-            // split search: lane i tests e[i] for i in [l, n-1)
-            const float di = s.d[c], di1 = s.d[c + 1 < N ? c + 1 : c], ei = s.e[c];
-            const bool small = c >= l && c + 1 < nn &&
-                               (fabsf(ei) <= kEps * (fabsf(di) + fabsf(di1)) || fabsf(ei) < kSafeMin);
-            uint64_t mask = __ballot(small);
-            if (N < 64) mask = (mask >> (g * N)) & ((1ull << N) - 1);
-            const int m = mask ? __ffsll((unsigned long long)mask) - 1 : nn - 1;
-            if (m == l) break;
-            if (iters >= budget) {
-                converged = false;
-                break;
+        for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)(mat * 64 + c), (uint32_t)k) : 0.0f;
+        // close eigenvalues: lanes cs .. c with gaps <= kOrtol |T|
+        const float prev = __shfl_up(lam, 1, N);
+        const bool brk = c == 0 || !mine || lam - prev > kOrtol * tnorm;
+        uint64_t brks = __ballot(brk);
+        if (N < 64) brks = (brks >> (g * N)) & ((1ull << N) - 1);
+        const int cs = 63 - __clzll((unsigned long long)(brks & ((2ull << c) - 1)));
+        const int pos = c - cs;
+        int rounds = pos;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
+        for (int pass = 0; pass < 2; ++pass) {
+            float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
+            uint64_t sw = 0;
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                if (k + 1 < N) {
+                    const float ek = s.e[k];
+                    const float an = s.d[k + 1] - lam, cn = s.e[k + 1], b1 = x[k + 1];
+                    const bool keep = fabsf(a) >= fabsf(ek);
+                    const float piv = keep ? a : ek;
+                    const float r0 = __builtin_amdgcn_rcpf(fabsf(piv) < tol ? copysignf(tol, piv) : piv);
+                    const float l = (keep ? ek : a) * r0;
+                    x[k] = (keep ? b0 : b1) * r0;
+                    u[k] = cc * r0;
+                    sw |= keep ? 0ull : (1ull << k);
+                    const float na = keep ? fmaf(-l, cc, an) : fmaf(-l, an, cc);
+                    cc = keep ? cn : -l * cn;
+                    b0 = keep ? fmaf(-l, b0, b1) : fmaf(-l, b1, b0);
+                    a = na;
+                } else {
+                    x[k] = b0 * __builtin_amdgcn_rcpf(fabsf(a) < tol ? copysignf(tol, a) : a);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            ++iters;
-            // the shift, from the 2x2 at the block's top
-            const float dl = s.d[l], dl1 = s.d[l + 1], el = s.e[l], dm = s.d[m];
-            float gg = (dl1 - dl) / (2.0f * el);
-            float rr = sqrtf(fmaf(gg, gg, 1.0f));
-            gg = dm - dl + el / (gg + copysignf(rr, gg));
-            float cs = 1.0f, sn = 1.0f, p = 0.0f;
-            bool stop = false;
+            // reload d, e from LDS below rather than keep the forward
+            // loop's copies live across it, and read the swaps from sw
+            // rather than keep every step's comparison mask
+            __asm__ volatile("" : "+v"(sw) : : "memory");
+            float x1 = 0.0f, x2 = 0.0f;
 #pragma unroll
-            for (int i = N - 2; i >= 0; --i) {
-                if (i >= l && i < m && !stop) {
-                    float f = sn * ee[i];
-                    const float b = cs * ee[i];
-                    // (c, s) from (g, f) as a plane rotation.  Tiny pairs are
-                    // scaled by a power of two first (group-uniform, rare), so
-                    // that f^2 + g^2 is never subnormal: rsqrt of a subnormal
-                    // is not accurate.
-                    float ga = gg, up = 1.0f;
-                    const float mx = fmaxf(fabsf(f), fabsf(gg));
-                    if (mx < 0x1p-50f && mx > 0.0f) {
-                        int eb = 0;
-                        (void)frexpf(mx, &eb);
-                        f = ldexpf(f, -eb);
-                        ga = ldexpf(gg, -eb);
-                        up = ldexpf(1.0f, eb);
-                    }
-                    const float h = fmaf(f, f, ga * ga);
-                    if (h == 0.0f) {
-                        // underflow: d[i+1] -= p and restart (e[m] already zero)
-                        dd[i + 1] -= p;
-                        ee[i + 1] = 0.0f;
-                        s.d[i + 1] = dd[i + 1];
-                        s.e[i + 1] = 0.0f;
-                        stop = true;
-                    } else {
-                        const float rinv = rsqrtf(h);
-                        const float ri = rinv * fmaf(-0.5f * h * rinv, rinv, 1.5f);   // one Newton step
-                        const float r = h * ri * up;
-                        ee[i + 1] = (i == m - 1) ? 0.0f : r;
-                        s.e[i + 1] = ee[i + 1];
-                        sn = f * ri;
-                        cs = ga * ri;
-                        gg = dd[i + 1] - p;
-                        const float t = fmaf(dd[i] - gg, sn, 2.0f * cs * b);
-                        p = sn * t;
-                        dd[i + 1] = gg + p;
-                        s.d[i + 1] = dd[i + 1];
-                        gg = fmaf(cs, t, -b);
-                        if (VEC) {
-                            const float z1 = x[i + 1];
-                            x[i + 1] = fmaf(sn, x[i], cs * z1);
-                            x[i] = fmaf(cs, x[i], -sn * z1);
-                        }
-                        if (i == l) {
-                            dd[i] -= p;
-                            ee[i] = gg;
-                            s.d[i] = dd[i];
-                            s.e[i] = gg;
-                        }
-                    }
+            for (int k = N - 1; k >= 0; --k) {
+                float xv = x[k];
+                if (k + 1 < N) {
+                    const bool swapped = (sw >> k) & 1;
+                    const float rk = s.re[k];
+                    const float q1 = swapped ? (s.d[k + 1] - lam) * rk : u[k];
+                    const float q2 = swapped ? s.e[k + 1] * rk : 0.0f;
+                    xv = fmaf(-q2, x2, fmaf(-q1, x1, xv));
+                }
+                x[k] = xv;
+                x2 = x1;
+                x1 = xv;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            normalize<N>(x);
+            // modified Gram-Schmidt within each close group, one member per
+            // round: the member at position t is final when round t begins
+            for (int t = 0; t < rounds; ++t) {
+                if (pos == t) normalize<N>(x);
+                const int src = g * N + min(cs + t, N - 1);
+                float dot = 0.0f;
+#pragma unroll
+                for (int k = 0; k < N; ++k) {
+                    u[k] = __shfl(x[k], src, 64);
+                    dot = fmaf(u[k], x[k], dot);
+                }
+                if (pos > t) {
+#pragma unroll
+                    for (int k = 0; k < N; ++k) x[k] = fmaf(-dot, u[k], x[k]);
                 }
             }
-            wave_lds_sync();
+            normalize<N>(x);
         }
-    }
 
-    // 5. ascending order: rank of each value (ties by index)
-    if (c < nn) {
-        const float dc = s.d[c];
-        int rank = 0;
-        for (int i = 0; i < nn; ++i) {
-            const float di = s.d[i];
-            rank += (di < dc) || (di == dc && i < c);
-        }
-        s.perm[rank] = c;
-        if (live) W[mat * n + rank] = bad ? qnan() : ldexpf(dc, ex);
-    }
-    if (live && info && c == 0) {
-        info[mat] = bad ? (1u << 17) : ((uint32_t)(iters < 0xFFFF ? iters : 0xFFFF) | (converged ? 1u << 16 : 0u));
-    }
-    if (VEC) {
-        wave_lds_sync();
-        // rows of Q through LDS, so that each lane writes one output column
-#pragma unroll
-        for (int j = 0; j < N; ++j) s.vs[c][j] = x[j];
-        wave_lds_sync();
-        if (live && c < nn) {
-            const int j = s.perm[c];
+        // 7. back to A's basis; lane c writes column c of V
+        backtransform_step<N - 3, N>(x, s, nn);
+        if (live && mine) {
             float* dst = V + mat * per;
 #pragma unroll
             for (int r = 0; r < N; ++r)
-                if (r < nn) dst[(size_t)r * n + c] = bad ? qnan() : s.vs[r][j];
+                if (r < nn) dst[(size_t)r * n + c] = bad ? qnan() : x[r];
         }
     }
+    if (live && mine) W[mat * n + c] = bad ? qnan() : ldexpf(lam, ex);
+    if (live && info && c == 0)
+        info[mat] = bad ? (1u << 17) : ((uint32_t)steps | (1u << 16));
 }
 
 template <int N, bool VEC>

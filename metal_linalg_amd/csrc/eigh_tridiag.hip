@@ -96,15 +96,6 @@ struct Cluster {         // consecutive slots of one block, close together
     int first, count;    // slots first .. first + count - 1
 };
 
-__device__ __forceinline__ float hash_uniform(unsigned a, unsigned b) {
-    unsigned x = a * 0x9E3779B1u ^ (b + 0x7F4A7C15u) * 0x85EBCA77u;
-    x ^= x >> 15;
-    x *= 0x2C1B3C6Du;
-    x ^= x >> 12;
-    x *= 0x297A2D39u;
-    x ^= x >> 15;
-    return (float)(x >> 8) * (2.0f / 16777216.0f) - 1.0f;   // (-1, 1)
-}
 
 // One thread per cluster.  Z[r * ldz + slot] holds the vectors (rows of
 // the block; the thread also zeroes the rest of its columns).  U is scratch
