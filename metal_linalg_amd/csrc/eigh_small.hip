@@ -323,8 +323,8 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         // (slagtf), the right-hand side carried along.  x[k] holds the
         // right-hand side, then row k of U scaled by its pivot (x, and u =
         // the superdiagonal entry where row k kept its place), then the
-        // solution.  Where rows k and k+1 were swapped (bit k of sw), U's row
-        // is (e_k, d_{k+1} - lam, e_{k+1}), rebuilt from LDS on the way back.
+        // solution.  Where rows k and k+1 were swapped (u = NaN), U's row is
+        // (e_k, d_{k+1} - lam, e_{k+1}), rebuilt from LDS on the way back.
         // The whole tridiagonal is solved: at a split (e = 0) the
         // elimination decouples, and rows past n (kPad, e = 0) carry zeros.
         // Eigenvectors of other blocks with an eigenvalue as close as this
@@ -345,7 +345,6 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
         for (int pass = 0; pass < 2; ++pass) {
             float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
-            uint64_t sw = 0;
 #pragma unroll
             for (int k = 0; k < N; ++k) {
                 if (k + 1 < N) {
@@ -356,8 +355,10 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
                     const float r0 = __builtin_amdgcn_rcpf(fabsf(piv) < tol ? copysignf(tol, piv) : piv);
                     const float l = (keep ? ek : a) * r0;
                     x[k] = (keep ? b0 : b1) * r0;
-                    u[k] = cc * r0;
-                    sw |= keep ? 0ull : (1ull << k);
+                    u[k] = keep ? cc * r0 : qnan();   // NaN marks a swap
+                    // pinned: computed here, not sunk into the backward loop
+                    // with their factors kept live instead
+                    __asm__ volatile("" : "+v"(x[k]), "+v"(u[k]));
                     const float na = keep ? fmaf(-l, cc, an) : fmaf(-l, an, cc);
                     cc = keep ? cn : -l * cn;
                     b0 = keep ? fmaf(-l, b0, b1) : fmaf(-l, b1, b0);
@@ -368,21 +369,21 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
                 __builtin_amdgcn_sched_barrier(0);
             }
             // reload d, e from LDS below rather than keep the forward
-            // loop's copies live across it, and read the swaps from sw
-            // rather than keep every step's comparison mask
-            __asm__ volatile("" : "+v"(sw) : : "memory");
+            // loop's copies live across it
+            __asm__ volatile("" ::: "memory");
             float x1 = 0.0f, x2 = 0.0f;
 #pragma unroll
             for (int k = N - 1; k >= 0; --k) {
                 float xv = x[k];
                 if (k + 1 < N) {
-                    const bool swapped = (sw >> k) & 1;
-                    const float rk = s.re[k];
-                    const float q1 = swapped ? (s.d[k + 1] - lam) * rk : u[k];
-                    const float q2 = swapped ? s.e[k + 1] * rk : 0.0f;
+                    const float rk = s.re[k], dk1 = s.d[k + 1], ek1 = s.e[k + 1];
+                    const bool swapped = u[k] != u[k];
+                    const float q1 = swapped ? (dk1 - lam) * rk : u[k];
+                    const float q2 = swapped ? ek1 * rk : 0.0f;
                     xv = fmaf(-q2, x2, fmaf(-q1, x1, xv));
                 }
                 x[k] = xv;
+                __asm__ volatile("" : "+v"(x[k]));
                 x2 = x1;
                 x1 = xv;
                 __builtin_amdgcn_sched_barrier(0);
