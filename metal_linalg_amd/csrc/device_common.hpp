@@ -39,6 +39,44 @@ __device__ __forceinline__ int group_or(int x) {
     return x;
 }
 
+// DPP sums within a wave64 (row = 16 lanes): quad_sum leaves every lane of
+// each group of 4 with the group's sum, half_row_sum groups of 8, row_sum
+// rows of 16; wave_sum returns the wave's sum (uniform, from lane 63 after
+// the row_bcast15 / row_bcast31 steps).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+    v = dpp_add<0xB1>(v);      // quad_perm [1,0,3,2]
+    return dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+}
+
+__device__ __forceinline__ float half_row_sum(float v) { return dpp_add<0x141>(quad_sum(v)); }   // row_half_mirror
+
+__device__ __forceinline__ float dpp_row_sum(float v) { return dpp_add<0x140>(half_row_sum(v)); }   // row_mirror
+
+__device__ __forceinline__ float wave_sum_f(float v) {
+    v = dpp_row_sum(v);
+    v = dpp_add<0x142, 0xa>(v);   // row_bcast15 into rows 1 and 3
+    v = dpp_add<0x143, 0xc>(v);   // row_bcast31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over an aligned group of G lanes (G = 8, 16, 32 or 64) on every lane of
+// the group, by DPP (one cross-lane permute for G = 32).
+template <int G>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+    if constexpr (G == 64) return wave_sum_f(v);
+    else if constexpr (G == 32) {
+        v = dpp_row_sum(v);
+        return v + __shfl_xor(v, 16, 32);
+    } else if constexpr (G == 16) return dpp_row_sum(v);
+    else if constexpr (G == 8) return half_row_sum(v);
+    else return group_sum<G>(v);
+}
+
 // Power-of-two exponent e with amax * 2^-e in [0.5, 1) (frexp's), 0 for a
 // zero or non-finite amax: the reference's scaled_input rule
 // (src/metal_runtime.mm:179-215).

@@ -43,15 +43,6 @@ constexpr int kColRows = 64;                   // rows per workgroup in sytrd_co
 constexpr int kSymvRows = 16;                  // rows per workgroup in sytrd_symv (16 lanes per row)
 constexpr float kTinySumsq = 8.271806e-25f;    // 2^-80
 
-__device__ __forceinline__ float dpp_row_sum(float v) {
-    // every lane of each row of 16 ends with the row's sum
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, false));
-    return v;
-}
-
 // ---- scan of the read triangle, scaled symmetric copy ----
 
 __global__ __launch_bounds__(256) void sym_scan_kernel(const float* __restrict__ a, int n, int lower,
@@ -122,19 +113,7 @@ struct SytrdArgs {
     int update;        // 0: only materialise W[:, i-1] (end of a panel)
 };
 
-__device__ __forceinline__ float quad_sum(float v) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
-    return v;
-}
 
-// the wave's sum, in every lane
-__device__ __forceinline__ float wave_sum_f(float v) {
-    v = dpp_row_sum(v);
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));   // row_bcast15
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));   // row_bcast31
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
 // 64 rows per workgroup, 4 threads per row; thread `sub` of a row takes the
 // panel columns k = sub, sub + 4, ...  Every global load of a thread is

@@ -46,8 +46,11 @@ constexpr int kMaxBisect = 64;
 
 template <int N>
 struct alignas(16) EighLds {
-    float vs[N][N + 1];   // staging of the read triangle, then the reflectors v_k (row k)
-    float bc[N + 4];      // per-step broadcast (v, then w)
+    union {
+        float stage[N][N + 1];   // the read triangle, mirrored through here
+        float vs[N][N + 4];      // the reflectors: v_k is row k (v_k[k+1] = 1)
+    };
+    float bc[2][N + 4];          // w of the rank-2 update, alternate steps
     float d[N + 4];       // the tridiagonal, rows >= n padded with kPad
     float e[N + 4];       // e[k] couples rows k and k+1; zero at splits and from row n - 1 on
     float f[N + 4];       // f[k] = e[k-1]^2, f[0] = 0
@@ -71,55 +74,58 @@ __device__ __forceinline__ float dot_tail(const float* x, const float* y) {
 
 // ssytd2 (lower) step K: reflector from column K below the subdiagonal, then
 // the symmetric rank-2 update of the trailing block.
+// The value of lane `src` of the group, on every lane of the group.
+template <int N>
+__device__ __forceinline__ float group_bcast(float v, int src) {
+    if constexpr (N == 64) return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+    else return __shfl(v, src, N);
+}
+
+// ssytd2 (lower) step K.  Lane c holds column c of the working matrix, so
+// by symmetry row K of the trailing block is x[K] across the lanes: the
+// reflector's entries are formed lane-parallel (lane c scales its own
+// x[K]), written as row K of vs (which keeps them for the
+// back-transformation), and read back as a broadcast for the products.
+// Then the symmetric rank-2 update of the trailing block, w through bc.
 template <int K, int N>
 __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c, int n) {
     if constexpr (K + 2 < N) {
         if (K + 2 < n) {
-            if (c == K) {
-                const float alpha = x[K + 1];
-                const float ss = dot_tail<K + 2, N>(x, x);
-                float beta = alpha, tau = 0.0f, scale = 1.0f;
-                if (ss >= kTinySumsq) {
-                    beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-                    tau = (beta - alpha) / beta;
-                    scale = 1.0f / (alpha - beta);
-                }
-                s.d[K] = x[K];
-                s.e[K] = beta;
-                s.tau[K] = tau;
-                x[K + 1] = 1.0f;
-                s.bc[K + 1] = 1.0f;
-#pragma unroll
-                for (int r = K + 2; r < N; ++r) {
-                    x[r] *= scale;
-                    s.bc[r] = x[r];
-                }
-            }
-            wave_lds_sync();
-            const float tau = s.tau[K];
-            float v[N];
-#pragma unroll
-            for (int r = K + 1; r < N; ++r) v[r] = s.bc[r];
-            // c laundered: otherwise the compiler precomputes this lane mask
-            // for every step at kernel entry and spills the SGPR pairs
+            // c laundered: otherwise the compiler precomputes the lane masks
+            // below for every step at kernel entry and spills the SGPR pairs
             int cl = c;
             __asm__ volatile("" : "+v"(cl));
-            const bool act = cl > K && cl < n;
-            float p = 0.0f, vc = 0.0f;
-            if (act) {
-                vc = s.bc[c];
-                p = tau * dot_tail<K + 1, N>(v, x);
+            const float xk = x[K];
+            const float alpha = group_bcast<N>(xk, K + 1);
+            const float ss = group_sum_dpp<N>(cl > K + 1 && cl < n ? xk * xk : 0.0f);
+            float beta = alpha, tau = 0.0f, scale = 1.0f;
+            if (ss >= kTinySumsq) {
+                beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
+                tau = (beta - alpha) / beta;
+                scale = 1.0f / (alpha - beta);
             }
-            const float half = 0.5f * tau * group_sum<N>(p * vc);
-            const float w = fmaf(-half, vc, p);
+            const bool act = cl > K && cl < n;
+            const float vc = cl == K + 1 ? 1.0f : (act ? xk * scale : 0.0f);
+            s.vs[K][c] = vc;
+            if (cl == K) {
+                s.d[K] = xk;
+                s.e[K] = beta;
+                s.tau[K] = tau;
+            }
             wave_lds_sync();
-            if (act) s.bc[c] = w;
+            float v[N];
+#pragma unroll
+            for (int r = K + 1; r < N; ++r) v[r] = s.vs[K][r];
+            const float p = act ? tau * dot_tail<K + 1, N>(v, x) : 0.0f;
+            const float half = 0.5f * tau * group_sum_dpp<N>(p * vc);
+            const float w = fmaf(-half, vc, p);
+            float* bc = s.bc[K & 1];
+            bc[c] = w;
             wave_lds_sync();
             if (act) {
 #pragma unroll
-                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-v[r], w, fmaf(-s.bc[r], vc, x[r]));
+                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-v[r], w, fmaf(-bc[r], vc, x[r]));
             }
-            wave_lds_sync();
         }
         tridiag_step<K + 1, N>(x, s, c, n);
     }
@@ -213,7 +219,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
             v = src[(size_t)r * n + c];
             amax = fmaxf(amax, fabsf(v));
             bad |= !finite_f(v);
-            s.vs[r][c] = v;
+            s.stage[r][c] = v;
         }
         x[r] = v;
     }
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
 #pragma unroll
     for (int r = 0; r < N; ++r) {
         const bool take = lower ? r >= c : r <= c;
-        if (live && r < nn && c < nn && !take) x[r] = s.vs[c][r];
+        if (live && r < nn && c < nn && !take) x[r] = s.stage[c][r];
     }
     amax = group_max<N>(amax);
     bad = group_or<N>(bad);
@@ -246,13 +252,6 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         if (c == nn - 1) {
             s.d[c] = diag;
             s.e[c] = 0.0f;
-        }
-    }
-    if (VEC) {
-        if (c + 2 < nn) {
-#pragma unroll
-            for (int r = 0; r < N; ++r)
-                if (r > c) s.vs[c][r] = x[r];
         }
     }
     wave_lds_sync();
