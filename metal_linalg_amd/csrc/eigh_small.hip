@@ -56,6 +56,7 @@ struct alignas(16) EighLds {
     float f[N + 4];       // f[k] = e[k-1]^2, f[0] = 0
     float re[N + 4];      // 1 / e[k] (0 where e[k] = 0)
     float tau[N];
+    int perm[N];
 };
 
 // sum of x[r] * y[r] over r in [LO, N), four partial sums
@@ -207,20 +208,22 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     const size_t per = (size_t)n * n;
 
     // 1. the read triangle, mirrored into a full symmetric matrix
+    // Every row is loaded unconditionally (clamped into the matrix) so that
+    // the N loads are all in flight together; the unread triangle's values
+    // are discarded by the selects.
     float x[N];
     float amax = 0.0f;
     int bad = 0;
-    const float* src = A + mat * per;
+    const float* src = A + (live ? mat : 0) * per + (c < nn ? c : nn - 1);
+#pragma unroll
+    for (int r = 0; r < N; ++r) x[r] = src[(size_t)(r < nn ? r : nn - 1) * n];
 #pragma unroll
     for (int r = 0; r < N; ++r) {
-        float v = 0.0f;
-        const bool take = lower ? r >= c : r <= c;
-        if (live && r < nn && c < nn && take) {
-            v = src[(size_t)r * n + c];
-            amax = fmaxf(amax, fabsf(v));
-            bad |= !finite_f(v);
-            s.stage[r][c] = v;
-        }
+        const bool take = live && r < nn && c < nn && (lower ? r >= c : r <= c);
+        const float v = take ? x[r] : 0.0f;
+        amax = fmaxf(amax, fabsf(v));
+        bad |= take && !finite_f(v);
+        s.stage[r][c] = v;
         x[r] = v;
     }
     wave_lds_sync();
@@ -293,11 +296,30 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     const float slack = 2.1f * 2.0f * kEps * tnorm * (float)nn + 4.2f * pivmin;
     const float atol = fmaxf(kEps * tnorm, 2.0f * pivmin);
 
+    // A diagonal T (every coupling split, e.g. A = a multiple of I, or the
+    // zero matrix of a non-finite input): its eigenpairs are (d_j, e_j)
+    // with j ranked by d (ties by index), exactly.  Waves holding only such
+    // groups skip the bisection and the inverse iteration.
+    const bool diag = nn == 1 || splits == ((1ull << (nn - 1)) - 1);
+    const bool all_diag = __ballot(!diag) == 0;
+    int row = c;
+    if (diag && c < nn) {
+        const float dc = s.d[c];
+        int rank = 0;
+        for (int i = 0; i < nn; ++i) {
+            const float di = s.d[i];
+            rank += (di < dc) || (di == dc && i < c);
+        }
+        s.perm[rank] = c;
+    }
+    wave_lds_sync();
+    if (diag && c < nn) row = s.perm[c];
+
     // 4. bisection: lane c brackets the c-th smallest eigenvalue
     const bool mine = c < nn;
     float lo = glo - slack, hi = ghi + slack;
     int steps = 0;
-    while (steps < kMaxBisect) {
+    while (!all_diag && steps < kMaxBisect) {
         const float mid = 0.5f * (lo + hi);
         const int cm = sturm_count<N>(s, mid, pivmin);
         if (cm > c) {
@@ -316,6 +338,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         const float up = __shfl_up(lam, off, N);
         if (c >= off) lam = fmaxf(lam, up);
     }
+    if (diag) lam = s.d[row];
 
     if (VEC) {
         // 5. inverse iteration: T - lam I = P L U with partial pivoting
@@ -334,7 +357,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)(mat * 64 + c), (uint32_t)k) : 0.0f;
         // close eigenvalues: lanes cs .. c with gaps <= kOrtol |T|
         const float prev = __shfl_up(lam, 1, N);
-        const bool brk = c == 0 || !mine || lam - prev > kOrtol * tnorm;
+        const bool brk = c == 0 || !mine || diag || lam - prev > kOrtol * tnorm;
         uint64_t brks = __ballot(brk);
         if (N < 64) brks = (brks >> (g * N)) & ((1ull << N) - 1);
         const int cs = 63 - __clzll((unsigned long long)(brks & ((2ull << c) - 1)));
@@ -342,7 +365,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         int rounds = pos;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
-        for (int pass = 0; pass < 2; ++pass) {
+        for (int pass = 0; pass < (all_diag ? 0 : 2); ++pass) {
             float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
 #pragma unroll
             for (int k = 0; k < N; ++k) {
@@ -405,6 +428,11 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
                 }
             }
             normalize<N>(x);
+        }
+
+        if (diag) {
+#pragma unroll
+            for (int k = 0; k < N; ++k) x[k] = k == row ? 1.0f : 0.0f;
         }
 
         // 7. back to A's basis; lane c writes column c of V
