@@ -53,118 +53,259 @@ __global__ __launch_bounds__(256) void copy_transpose_kernel(const float* __rest
 }
 
 // One workgroup factors the nb x nb diagonal block (nb <= 128, padded to 128
-// with the identity) and forms the inverse X = L^-1 of its factor in the same
-// sweep.  Thread t owns the 8 x 8 blocks at block row bi = t >> 4 and block
-// column bj = t & 15 of both A (a[i][j] = A[8 bi + i][8 bj + j]) and X.
-//
-// Step k: the threads of block column k / 8 publish their A blocks to LDS
-// transposed (so column k is contiguous), the threads of block row k / 8
-// their X blocks (so row k is contiguous).  With d = A[k][k],
-// inv = 1 / sqrt(d) and g = inv^2, every thread then applies
-//   a[i][j] -= A[r][k] * lc(c),      x[i][j] -= lc(r) * X[k][c],
-//   lc(q) = A[q][k] g (q > k),  1 - inv (q = k),  0 (q < k)
-// (r = 8 bi + i, c = 8 bj + j; A[r][k] taken as 0 for r < k).  For the
-// columns right of k this is the right-looking update
-// A[r][c] -= L[r][k] L[c][k]; on column k it scales to L[r][k] = A[r][k] inv;
-// on X it scales row k by inv and performs the forward substitution
-// X[r] -= L[r][k] X[k] for the rows below.  Entries above the diagonal of A
-// pick up one finite value each (row k, from A[k][k]) that is never read
-// again: the output takes the lower triangle, the diagonal from the saved
-// pivots.  X stays exactly lower triangular.  The published blocks alternate between two LDS slots, so one
-// barrier per step suffices: a slot is rewritten two steps later, after
-// every thread has passed the barrier that follows its reads.
+// with the identity) in LDS and forms the inverse X = L^-1 of its factor, in
+// four sub-panels of 32 columns (right-looking within the block):
+//   1. wave 0 factors the 32 x 32 diagonal sub-block, lane r holding row r:
+//      per column k the pivot and the scaled column are read across lanes
+//      (readlane, so no LDS round trip or barrier per column), and the same
+//      column values drive, in lanes 32..63, the forward substitution that
+//      builds the sub-block's inverse Y (lane 32 + c holding column c);
+//   2. the rows below, within the block: L = A Y^T (all threads);
+//   3. the trailing lower triangle of the block: A -= L L^T (4 x 4 tiles);
+// then the off-diagonal 32 x 32 blocks of X, by block forward substitution:
+// X_ip = -Y_i sum_{k=p}^{i-1} L_ik X_kp, in rounds of i - p = 1, 2, 3.
+// Barriers: a handful per sub-panel instead of one per column.
 //
 // The first pivot that is not positive and finite sets info = j0 + k + 1
-// (unless an earlier block already set it); the block carries on with NaN,
-// which the final extract turns into the all-NaN output.
-struct DiagSlot {
-    float a[8][NB];   // a[j][r] = A[r][8 kb + j]: block column kb, transposed
-    float x[8][NB];   // x[i][c] = X[8 kb + i][c]: block row kb
+// (unless an earlier block already set it); the factorisation carries on with
+// NaN, which the final extract turns into the all-NaN output.
+constexpr int SB = 32;           // sub-panel width
+constexpr int DT = 256;          // threads of the diagonal-block kernel
+constexpr int LDA = NB + 4;      // LDS row stride: rows 16-byte aligned
+
+struct DiagLds {
+    float A[NB][LDA];            // the block, then its factor L (lower)
+    float X[NB][LDA];            // X = L^-1 (lower), zero above
+    float S[3][SB][SB + 4];      // block products of one round
+    int fail;
 };
 
-__global__ __launch_bounds__(256) void chol_diag_kernel(float* __restrict__ W, int ld, int j0, int nb,
-                                                        float* __restrict__ X, uint32_t* __restrict__ info) {
-    __shared__ DiagSlot slot[2];
-    __shared__ float piv[NB];
-    const int t = threadIdx.x;
-    const int bi = t >> 4, bj = t & 15;
-    const int r0 = 8 * bi, c0 = 8 * bj;
-    float a[8][8], x[8][8];
+// acc (4 x 4) += P[r0 .. r0+3][0 .. 31] Q[0 .. 31][c0 .. c0+3]: P and Q are
+// 32 x 32 blocks with row strides ldp and ldq.
+__device__ __forceinline__ void tile_mm(float (&acc)[4][4], const float* P, int ldp, const float* Q, int ldq, int r0,
+                                        int c0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int q0 = 0; q0 < SB; q0 += 4) {
+        float pr[4][4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int r = r0 + i, c = c0 + j;
-            // unconditional load from a clamped address, then masked: all 64
-            // loads are in flight before the first wait
-            const bool in = r < nb && c < nb && c <= r;
-            const float v = W[in ? (size_t)(j0 + r) * ld + j0 + c : (size_t)j0 * ld + j0];
-            a[i][j] = in ? v : (r == c && (r >= nb || c >= nb) ? 1.0f : 0.0f);
-            x[i][j] = r == c ? 1.0f : 0.0f;
+        for (int i = 0; i < 4; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(P + (r0 + i) * ldp + q0);
+            pr[i][0] = v.x;
+            pr[i][1] = v.y;
+            pr[i][2] = v.z;
+            pr[i][3] = v.w;
         }
-    int fail = 0;
-    for (int k = 0; k < NB; ++k) {
-        DiagSlot& S = slot[k & 1];
-        const int kb = k >> 3, kk = k & 7;
-        if (bj == kb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 qv = *reinterpret_cast<const float4*>(Q + (q0 + q) * ldq + c0);
+            const float qq[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(pr[i][q], qq[j], acc[i][j]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(DT) void chol_diag_kernel(float* __restrict__ W, int ld, int j0, int nb,
+                                                       float* __restrict__ Xout, uint32_t* __restrict__ info) {
+    __shared__ DiagLds D;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    // the lower triangle, padded with the identity.  Thread t takes column
+    // c = t % 128 of rows t / 128 + 2 i; every load is issued unconditionally
+    // from a clamped address (then masked), 16 in flight per batch.
+    const int cc = t & (NB - 1), rb = t >> 7;
+    const float* src = W + (size_t)j0 * ld + j0 + (cc < nb ? cc : nb - 1);
+#pragma unroll
+    for (int i0 = 0; i0 < NB / 2; i0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = rb + 2 * (i0 + i);
+            v[i] = src[(size_t)(r < nb ? r : nb - 1) * ld];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = rb + 2 * (i0 + i);
+            const bool in = r < nb && cc < nb && cc <= r;
+            D.A[r][cc] = in ? v[i] : (r == cc ? 1.0f : 0.0f);
+            D.X[r][cc] = 0.0f;
+        }
+    }
+    if (t == 0) D.fail = 0;
+    __syncthreads();
+
+    for (int s0 = 0; s0 < NB; s0 += SB) {
+        // 1. the 32 x 32 diagonal sub-block and its inverse (wave 0).  Lane
+        // r < 32 holds row r of the sub-block (becoming row r of L), lane
+        // 32 + r column r of the identity (becoming column r of Y = L^-1):
+        // both take the same update, z[c] -= z[k] L[c][k], with L[c][k] read
+        // from lane c.
+        if (wv == 0) {
+            const int r = lane & (SB - 1);
+            const bool lrow = lane < SB;
+            float z[SB];
+#pragma unroll
+            for (int j = 0; j < SB; ++j) {
+                const float av = D.A[s0 + r][s0 + j];
+                z[j] = lrow ? (j <= r ? av : 0.0f) : (j == r ? 1.0f : 0.0f);
+            }
+            int failk = 0;
+#pragma unroll
+            for (int k = 0; k < SB; ++k) {
+                const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(z[k]), k));
+                if (failk == 0 && !(d > 0.0f && d <= FLT_MAX)) failk = k + 1;
+                // 1 / sqrt(d) by the hardware estimate and one Newton step
+                // (the critical path of the column chain), sqrt(d) = d / sqrt(d)
+                const float e0 = __builtin_amdgcn_rsqf(d);
+                const float ik = e0 * fmaf(-0.5f * d * e0, e0, 1.5f);
+                const float pk = d * ik;
+                // L[r][k] = A[r][k] / L[k][k] (r > k), L[k][k]; Y[k][.] final
+                z[k] = lrow && r == k ? pk : z[k] * ik;
+#pragma unroll
+                for (int c = k + 1; c < SB; ++c) {
+                    const float lck = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(z[k]), c));
+                    z[c] = fmaf(-z[k], lck, z[c]);
+                }
+            }
+            if (lrow) {
+#pragma unroll
+                for (int j = 0; j < SB; ++j)
+                    if (j <= r) D.A[s0 + r][s0 + j] = z[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < SB; ++j) D.X[s0 + j][s0 + r] = z[j];   // Y[j][r], zero for j < r
+            }
+            if (lane == 0 && failk != 0 && D.fail == 0) D.fail = s0 + failk;
+        }
+        __syncthreads();
+        const int mi = NB - s0 - SB;   // rows below the sub-block, within the block
+        if (mi <= 0) break;
+        // 2. L[i][s0 ..] = A[i][s0 ..] Y^T for the rows below: thread -> (row,
+        // 8 columns), at most two passes; results held over the barrier
+        float out[2][8];
+        int orow[2], ocol[2];
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const int idx = t + pass * DT;
+            const int i = s0 + SB + (idx >> 2), cg = (idx & 3) * 8;
+            orow[pass] = idx < mi * 4 ? i : -1;
+            ocol[pass] = cg;
+            const int ii = idx < mi * 4 ? i : s0 + SB;
+            float ar[SB];
+#pragma unroll
+            for (int k0 = 0; k0 < SB; k0 += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(&D.A[ii][s0 + k0]);
+                ar[k0] = v.x;
+                ar[k0 + 1] = v.y;
+                ar[k0 + 2] = v.z;
+                ar[k0 + 3] = v.w;
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                *reinterpret_cast<float4*>(&S.a[j][r0]) = make_float4(a[0][j], a[1][j], a[2][j], a[3][j]);
-                *reinterpret_cast<float4*>(&S.a[j][r0 + 4]) = make_float4(a[4][j], a[5][j], a[6][j], a[7][j]);
-            }
-        }
-        if (bi == kb) {
+                const float* yr = &D.X[s0 + cg + j][s0];
+                float acc = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                *reinterpret_cast<float4*>(&S.x[i][c0]) = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
-                *reinterpret_cast<float4*>(&S.x[i][c0 + 4]) = make_float4(x[i][4], x[i][5], x[i][6], x[i][7]);
+                for (int k0 = 0; k0 < SB; k0 += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(yr + k0);
+                    acc = fmaf(ar[k0], v.x, acc);
+                    acc = fmaf(ar[k0 + 1], v.y, acc);
+                    acc = fmaf(ar[k0 + 2], v.z, acc);
+                    acc = fmaf(ar[k0 + 3], v.w, acc);
+                }
+                out[pass][j] = acc;
             }
         }
         __syncthreads();
-        const float* colk = S.a[kk];   // column k of A
-        const float* rowk = S.x[kk];   // row k of X
-        const float d = colk[k];
-        if (fail == 0 && !(d > 0.0f && d <= FLT_MAX)) fail = k + 1;
-        const float p = sqrtf(d);
-        const float inv = 1.0f / p;
-        const float g = inv * inv, one = 1.0f - inv;
-        if (t == 0) piv[k] = p;
-        const float4 cr0 = *reinterpret_cast<const float4*>(&colk[r0]);
-        const float4 cr1 = *reinterpret_cast<const float4*>(&colk[r0 + 4]);
-        const float4 cc0 = *reinterpret_cast<const float4*>(&colk[c0]);
-        const float4 cc1 = *reinterpret_cast<const float4*>(&colk[c0 + 4]);
-        const float4 xr0 = *reinterpret_cast<const float4*>(&rowk[c0]);
-        const float4 xr1 = *reinterpret_cast<const float4*>(&rowk[c0 + 4]);
-        float cr[8] = {cr0.x, cr0.y, cr0.z, cr0.w, cr1.x, cr1.y, cr1.z, cr1.w};
-        const float cc[8] = {cc0.x, cc0.y, cc0.z, cc0.w, cc1.x, cc1.y, cc1.z, cc1.w};
-        const float xk[8] = {xr0.x, xr0.y, xr0.z, xr0.w, xr1.x, xr1.y, xr1.z, xr1.w};
-        float lr[8], lcol[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            lr[q] = r0 + q > k ? cr[q] * g : (r0 + q == k ? one : 0.0f);
-            lcol[q] = c0 + q > k ? cc[q] * g : (c0 + q == k ? one : 0.0f);
-            cr[q] = r0 + q < k ? 0.0f : cr[q];   // above the diagonal: not an entry of L
-        }
+        for (int pass = 0; pass < 2; ++pass)
+            if (orow[pass] >= 0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                a[i][j] = fmaf(-cr[i], lcol[j], a[i][j]);
-                x[i][j] = fmaf(-lr[i], xk[j], x[i][j]);
+                for (int j = 0; j < 8; ++j) D.A[orow[pass]][s0 + ocol[pass] + j] = out[pass][j];
             }
+        __syncthreads();
+        // 3. the trailing lower triangle: A[i][c] -= sum_k L[i][k] L[c][k],
+        // 4 x 4 tiles (tr >= tc) of the mi x mi block
+        const int tn = mi / 4, ntiles = tn * (tn + 1) / 2;
+        for (int idx = t; idx < ntiles; idx += DT) {
+            int tr = (int)((sqrtf(8.0f * (float)idx + 1.0f) - 1.0f) * 0.5f);
+            while ((tr + 1) * (tr + 2) / 2 <= idx) ++tr;
+            while (tr * (tr + 1) / 2 > idx) --tr;
+            const int tc = idx - tr * (tr + 1) / 2;
+            const int i0 = s0 + SB + 4 * tr, c0 = s0 + SB + 4 * tc;
+            float acc[4][4] = {};
+#pragma unroll
+            for (int k0 = 0; k0 < SB; k0 += 4) {
+                float li[4][4], lc[4][4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 u = *reinterpret_cast<const float4*>(&D.A[i0 + q][s0 + k0]);
+                    const float4 v = *reinterpret_cast<const float4*>(&D.A[c0 + q][s0 + k0]);
+                    li[q][0] = u.x; li[q][1] = u.y; li[q][2] = u.z; li[q][3] = u.w;
+                    lc[q][0] = v.x; lc[q][1] = v.y; lc[q][2] = v.z; lc[q][3] = v.w;
+                }
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(li[i][kk], lc[j][kk], acc[i][j]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (c0 + j <= i0 + i) D.A[i0 + i][c0 + j] -= acc[i][j];
+        }
+        __syncthreads();
     }
-    __syncthreads();   // piv complete
+
+    // X's off-diagonal blocks: round dd computes X_ip for i - p = dd
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = r0 + i;
+    for (int dd = 1; dd < NB / SB; ++dd) {
+        const int nblk = NB / SB - dd;   // blocks this round (<= 3)
+        // S_b = sum_{k=p}^{i-1} L_ik X_kp; thread -> one 4 x 4 tile of one block
+        if (t < nblk * 64) {
+            const int bidx = t >> 6, tile = t & 63;
+            const int p = bidx, i = p + dd;
+            const int r0 = (tile >> 3) * 4, c0 = (tile & 7) * 4;
+            float acc[4][4] = {};
+            for (int k = p; k < i; ++k)
+                tile_mm(acc, &D.A[i * SB][k * SB], LDA, &D.X[k * SB][p * SB], LDA, r0, c0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = c0 + j;
-            if (r < nb && c <= r) W[(size_t)(j0 + r) * ld + j0 + c] = r == c ? piv[r] : a[i][j];
-            if (r < nb && c < nb) X[(size_t)r * nb + c] = x[i][j];
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) D.S[bidx][r0 + q][c0 + j] = acc[q][j];
+        }
+        __syncthreads();
+        // X_ip = -Y_i S_b
+        if (t < nblk * 64) {
+            const int bidx = t >> 6, tile = t & 63;
+            const int p = bidx, i = p + dd;
+            const int r0 = (tile >> 3) * 4, c0 = (tile & 7) * 4;
+            float acc[4][4] = {};
+            tile_mm(acc, &D.X[i * SB][i * SB], LDA, &D.S[bidx][0][0], SB + 4, r0, c0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) D.X[i * SB + r0 + q][p * SB + c0 + j] = -acc[q][j];
+        }
+        __syncthreads();
+    }
+
+    // L (lower, diagonal included) back to W; X out (nb x nb)
+    if (cc < nb) {
+        float* dst = W + (size_t)j0 * ld + j0 + cc;
+#pragma unroll 8
+        for (int i = 0; i < NB / 2; ++i) {
+            const int r = rb + 2 * i;
+            if (r < nb) {
+                if (cc <= r) dst[(size_t)r * ld] = D.A[r][cc];
+                Xout[(size_t)r * nb + cc] = D.X[r][cc];
+            }
         }
     }
-    if (t == 0 && fail != 0 && *info == 0) *info = (uint32_t)(j0 + fail);
+    if (t == 0 && D.fail != 0 && *info == 0) *info = (uint32_t)(j0 + D.fail);
 }
 
 // out = the working lower triangle (or its transpose for `upper`), the
