@@ -171,7 +171,7 @@ __device__ __forceinline__ void qr_leaf_column(float (&a)[RPT][LW], QrLeafShared
         const int c = t >> 5, j = t & 31;   // 32 threads per column, 16 partials each
         float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < LT / 32; ++i) s += S.red[c][j * (LT / 32) + i];
+        for (int i = 0; i < LT / 32; ++i) s += S.red[c][i * 32 + j];   // lanes on consecutive banks
         s = dpp_add_halves(s);
         if (lane == 31 || lane == 63) S.dot[c] = s;
     }
@@ -263,19 +263,33 @@ __global__ __launch_bounds__(LT) void qr_leaf_kernel(float* __restrict__ P, int 
     }
     QrLeafColumns<0, RPT>::run(a, S, t, lane, wv, w);
 
-    // back to P, and V^T's rows
+    // back to P, and V^T's rows; a thread's G consecutive rows move as one
+    // 16-byte store where aligned and inside the leaf
+    const bool vst = vec && (ldv & 3) == 0;
 #pragma unroll
     for (int c = 0; c < LW; ++c) {
         if (c >= w) continue;
         float* col = P + (size_t)(cl + c) * ldp + cl;
         float* vrow = Vt + (size_t)(cl + c) * ldv + cl;
 #pragma unroll
-        for (int q = 0; q < RPT; ++q) {
-            const int li = R::row(t, q);
-            if (li < m) {
-                col[li] = a[q][c];
-                vrow[li] = li < c ? 0.0f : (li == c ? 1.0f : a[q][c]);
+        for (int q0 = 0; q0 < RPT; q0 += G) {
+            const int li = R::row(t, q0);
+            float vv[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) vv[g] = li + g < c ? 0.0f : (li + g == c ? 1.0f : a[q0 + g][c]);
+            if constexpr (G == 4) {
+                if (vst && li + 3 < m) {
+                    *reinterpret_cast<float4*>(col + li) = make_float4(a[q0][c], a[q0 + 1][c], a[q0 + 2][c], a[q0 + 3][c]);
+                    *reinterpret_cast<float4*>(vrow + li) = make_float4(vv[0], vv[1], vv[2], vv[3]);
+                    continue;
+                }
             }
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+                if (li + g < m) {
+                    col[li + g] = a[q0 + g][c];
+                    vrow[li + g] = vv[g];
+                }
         }
     }
     for (int idx = t; idx < w * cl; idx += LT) {   // V^T left of the leaf: zero
