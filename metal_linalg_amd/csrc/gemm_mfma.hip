@@ -79,27 +79,23 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ p, int ld, i
             }
         }
     } else {
-        // stored [k][row]: a row of 128 floats per k; thread t takes rows
-        // (t & 31) * 4 .. +3 of k = t >> 5 and of k + 8
-        const int rq = (t & 31) * 4;
+        // stored [k][row]: thread t takes row t % 128 of the tile at k =
+        // kb .. kb+3 and kb+8 .. kb+11 (kb = 4 (t / 128)).  Each load is a
+        // wave's 64 consecutive rows of one k (coalesced), and the thread
+        // ends with 4 consecutive k of one row: one conflict-free 16-byte
+        // LDS store each (a row-strided store of single floats would hit
+        // two banks only).
+        const int rr = t & (BM - 1), kb = (t >> 7) * 4;
+        const int r = r0 + rr;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int k = k0 + (t >> 5) + h * 8;
-            const int r = r0 + rq;
-            if (VEC) {
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int k = k0 + kb + h * 8 + i;
                 const bool in = k < K && r < rows;
-                const floatx4 v = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)k * ld + r : 0));
-#pragma unroll
-                for (int i = 0; i < 4; ++i) reg[h * 4 + i] = in ? v[i] : 0.0f;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool in = k < K && r + i < rows;
-                    const float x = p[in ? (size_t)k * ld + r + i : 0];
-                    reg[h * 4 + i] = in ? x : 0.0f;
-                }
+                const float x = p[in ? (size_t)k * ld + r : 0];
+                reg[h * 4 + i] = in ? x : 0.0f;
             }
-        }
     }
 }
 
@@ -116,12 +112,11 @@ __device__ __forceinline__ void store_tile(float (*s)[LP], const float (&reg)[8]
             *reinterpret_cast<floatx4*>(&s[r][kq]) = v;
         }
     } else {
-        const int rq = (t & 31) * 4;
+        const int rr = t & (BM - 1), kb = (t >> 7) * 4;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int k = (t >> 5) + h * 8;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s[rq + i][k] = reg[h * 4 + i];
+            floatx4 v = {reg[h * 4 + 0], reg[h * 4 + 1], reg[h * 4 + 2], reg[h * 4 + 3]};
+            *reinterpret_cast<floatx4*>(&s[rr][kb + h * 8]) = v;
         }
     }
 }
