@@ -57,6 +57,7 @@ struct alignas(16) EighLds {
     float re[N + 4];      // 1 / e[k] (0 where e[k] = 0)
     float tau[N];
     int perm[N];
+    int cnt[N];
 };
 
 // sum of x[r] * y[r] over r in [LO, N), four partial sums
@@ -315,10 +316,31 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     wave_lds_sync();
     if (diag && c < nn) row = s.perm[c];
 
-    // 4. bisection: lane c brackets the c-th smallest eigenvalue
+    // 4. bisection: lane c brackets the c-th smallest eigenvalue.  First
+    // one multisection pass: lane i counts at the i-th of N + 1 equal
+    // divisions of the Gershgorin interval, and every lane takes its bracket
+    // from those counts (the points with at most c, and more than c,
+    // eigenvalues below them); this replaces the first bisection steps, in
+    // which the lanes would all count at the same few points.
     const bool mine = c < nn;
-    float lo = glo - slack, hi = ghi + slack;
+    const float g0 = glo - slack, g1 = ghi + slack, gh = (g1 - g0) / (float)(N + 1);
+    float lo = g0, hi = g1;
     int steps = 0;
+    if (!all_diag) {
+        s.cnt[c] = sturm_count<N>(s, fmaf((float)(c + 1), gh, g0), pivmin);
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float xi = fmaf((float)(i + 1), gh, g0);
+            if (s.cnt[i] <= c) lo = fmaxf(lo, xi);
+            else hi = fminf(hi, xi);
+        }
+        if (!(lo < hi)) {   // counts not monotone in floating point: the whole interval
+            lo = g0;
+            hi = g1;
+        }
+        steps = 1;
+    }
     while (!all_diag && steps < kMaxBisect) {
         const float mid = 0.5f * (lo + hi);
         const int cm = sturm_count<N>(s, mid, pivmin);
