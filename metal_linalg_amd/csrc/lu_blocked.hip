@@ -91,6 +91,25 @@ struct LeafRows {
 // register index is a compile-time constant.  Every wave publishes its best
 // candidate key and that row; after the barrier every thread picks the
 // winner, so the pivot row arrives with the choice.
+// The source row of row x under the sequential swaps k <-> pl[k] for k =
+// 0 .. m-1, found by undoing them from the last; pl is read 8 entries at a
+// time so that the LDS reads overlap instead of one round trip per swap.
+__device__ __forceinline__ int undo_swaps(const int* pl, int m, int x) {
+    for (int k1 = m; k1 > 0;) {
+        const int k0 = k1 >= 8 ? k1 - 8 : 0;
+        int p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = pl[k0 + i < k1 ? k0 + i : k0];
+#pragma unroll
+        for (int i = 7; i >= 0; --i) {
+            const int k = k0 + i;
+            if (k < k1) x = x == k ? p[i] : (x == p[i] ? k : x);
+        }
+        k1 = k0;
+    }
+    return x;
+}
+
 template <int K, int RPT, int W>
 __device__ __forceinline__ void leaf_column(float (&a)[RPT][W], LeafShared& S, int t, int lane, int wv,
                                             int& zero_at) {
@@ -306,12 +325,7 @@ __global__ __launch_bounds__(LT) void lu_leaf_kernel(float* __restrict__ P, int 
             d = S.plist[t - w];
             if (d < w) d = -1;   // already an entry
         }
-        int x = d;
-        if (d >= 0)
-            for (int k = w - 1; k >= 0; --k) {
-                const int p = S.plist[k];
-                x = x == k ? p : (x == p ? k : x);
-            }
+        const int x = d >= 0 ? undo_swaps(S.plist, w, d) : d;
         edst[t] = d;
         esrc[t] = x;
     }
@@ -373,7 +387,7 @@ __global__ __launch_bounds__(LT) void lu_leaf_kernel(float* __restrict__ P, int 
 constexpr int kSwapCols = 32;
 
 __global__ __launch_bounds__(256) void lu_swap_kernel(float* __restrict__ A, int n, int pj, int pe,
-                                                      const uint32_t* __restrict__ piv) {
+                                                      const uint32_t* __restrict__ piv, int oc0, int oc1) {
     __shared__ int pl[NB];              // the panel's swap targets, relative to pj
     __shared__ int edst[2 * NB], esrc[2 * NB];
     __shared__ float stage[2 * NB][kSwapCols + 1];
@@ -388,18 +402,15 @@ __global__ __launch_bounds__(256) void lu_swap_kernel(float* __restrict__ A, int
         int d = -1;
         if (e < nbk) d = e;
         else if (e >= NB && e - NB < nbk && pl[e - NB] >= nbk) d = pl[e - NB];
-        int x = d;
-        if (d >= 0)
-            for (int k = nbk - 1; k >= 0; --k) {
-                const int p = pl[k];
-                x = x == k ? p : (x == p ? k : x);
-            }
+        const int x = d >= 0 ? undo_swaps(pl, nbk, d) : d;
         edst[e] = d;
         esrc[e] = x;
     }
     __syncthreads();
-    const int nout = n - nbk;   // columns outside the panel
-    const int c0 = blockIdx.x * kSwapCols;
+    // columns outside the panel, numbered oc = 0 .. n - nbk - 1 left to
+    // right; this launch moves oc0 .. oc1 - 1
+    const int nout = oc1;
+    const int c0 = oc0 + blockIdx.x * kSwapCols;
     // all loads first (clamped addresses), then the LDS writes
     constexpr int kIters = 2 * NB * kSwapCols / 256;
     float sv[kIters];
@@ -675,7 +686,7 @@ void lu_blocked_one(float* lu, uint32_t* piv, uint32_t* info, float* P, int n, h
         const int nout = n - nbk;
         if (nout > 0)
             hipLaunchKernelGGL(lu_swap_kernel, dim3((unsigned)cdiv(nout, kSwapCols)), dim3(256), 0, s, lu, n, pj, pe,
-                               piv);
+                               piv, 0, nout);
         if (pe < n) {
             const int nc = n - pe;
             hipLaunchKernelGGL((trsm_block_kernel<false, true>), dim3((unsigned)cdiv(nc, kTrsmCols)), dim3(256), 0, s,
@@ -706,12 +717,7 @@ __global__ __launch_bounds__(256) void compose_perm_kernel(const uint32_t* __res
         int d = -1;
         if (t < nbk) d = t;
         else if (t >= NB && t - NB < nbk && pl[t - NB] >= nbk) d = pl[t - NB];
-        int x = d;
-        if (d >= 0)
-            for (int k = nbk - 1; k >= 0; --k) {
-                const int p = pl[k];
-                x = x == k ? p : (x == p ? k : x);
-            }
+        const int x = d >= 0 ? undo_swaps(pl, nbk, d) : d;
         const int v = d >= 0 ? src[pj + x] : 0;
         __syncthreads();
         if (d >= 0) src[pj + d] = v;
