@@ -39,7 +39,7 @@ FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
 # x1.9998, WRITE_SIZE x1.0); the runs and the scaling are in
 # profiles/<kernel>_<workload>.md.  Workloads not yet counted report null.
 TRAFFIC_BYTES = {
-    "eigh": 54_815_459 + 68_295_067,   # profiles/eigh_small_eigh.md
+    "eigh": 74_606_375 + 68_292_919,   # profiles/eigh_small_eigh.md
     "qr": 42_169_219 + 81_920_000,     # profiles/qr_small_qr.md
 }
 
