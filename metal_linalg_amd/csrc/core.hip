@@ -133,6 +133,84 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
     call.finish();
 }
 
+namespace {
+
+// dst[b] (cols x rows) = src[b]^T (rows x cols), through 32 x 32 LDS tiles
+__global__ __launch_bounds__(256) void batch_transpose_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                              int rows, int cols) {
+    __shared__ float tile[32][33];
+    const size_t per = (size_t)rows * cols;
+    const float* S = src + blockIdx.z * per;
+    float* D = dst + blockIdx.z * per;
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int r = ty; r < 32; r += 8)
+        if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = S[(size_t)(r0 + r) * cols + c0 + tx];
+    __syncthreads();
+    for (int c = ty; c < 32; c += 8)
+        if (c0 + c < cols && r0 + tx < rows) D[(size_t)(c0 + c) * rows + r0 + tx] = tile[tx][c];
+}
+
+void batch_transpose(const float* src, float* dst, uint32_t batch, uint32_t rows, uint32_t cols, hipStream_t s) {
+    for (uint32_t b0 = 0; b0 < batch; b0 += 65535) {
+        const uint32_t nb = std::min<uint32_t>(65535, batch - b0);
+        const size_t off = (size_t)b0 * rows * cols;
+        hipLaunchKernelGGL(batch_transpose_kernel, dim3((unsigned)cdiv(cols, 32), (unsigned)cdiv(rows, 32), nb),
+                           dim3(256), 0, s, src + off, dst + off, (int)rows, (int)cols);
+    }
+}
+
+// Thin SVD of matrices with min(M, N) = K <= 64 beyond the batched kernel's
+// 128 rows: the tall problem A = Q R (blocked Householder QR), the SVD of the
+// K x K factor R = U_R S V^T (batched kernel), then U = Q U_R (MFMA GEMM).
+// A wide matrix is solved as its transpose.  Non-finite input reaches R as
+// NaN and gives NaN outputs with info bit 17; the flag bits and sweep counts
+// are those of R's SVD, which has A's singular values and right vectors.
+// The reference's tall route is the same factorisation on its CPU path
+// (src/svd.mm:772-890: sgeqrf, sgesdd on R, U = Q U_R).
+void svd_tall(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
+    const uint32_t M = a.rows, N = a.cols, B = a.batch;
+    const bool wide = M < N;
+    const uint32_t m = wide ? N : M, k = wide ? M : N;   // the tall problem: m x k
+    const bool vec = u != nullptr;
+    Call call;
+    hipStream_t st = call.stream();
+    const float* da = call.in(a.data, (size_t)B * M * N);
+    float* ds = call.out(s, (size_t)B * k);
+    float* du = vec ? call.out(u, (size_t)B * M * k) : nullptr;
+    float* dvt = vec ? call.out(vt, (size_t)B * k * N) : nullptr;
+    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+    const float* tall = da;
+    if (wide) {
+        float* at = call.tmp<float>((size_t)B * m * k);
+        batch_transpose(da, at, B, M, N, st);
+        tall = at;
+    }
+    float* q = vec ? call.tmp<float>((size_t)B * m * k) : nullptr;
+    float* r = call.tmp<float>((size_t)B * k * k);
+    float* qw = static_cast<float*>(call.scratch(qr_blocked_workspace(m, k)));
+    qr_blocked(tall, q, r, B, m, k, vec ? k : 0, k, qw, st);
+    float* ur = vec ? call.tmp<float>((size_t)B * k * k) : nullptr;
+    // right vectors of the tall problem: A's V^T, or (wide) A's U transposed
+    float* vtt = !vec ? nullptr : wide ? call.tmp<float>((size_t)B * k * k) : dvt;
+    float* ws = static_cast<float*>(call.scratch(svd_small_workspace(k, k, B)));
+    svd_small(r, ur, ds, vtt, di, ws, B, k, k, st);
+    if (vec) {
+        // left vectors of the tall problem, m x k: Q U_R
+        float* ut = wide ? call.tmp<float>((size_t)B * m * k) : du;
+        sgemm(false, false, (int)m, (int)k, (int)k, 1.0f, q, (int)k, (long long)m * k, ur, (int)k, (long long)k * k,
+              0.0f, ut, (int)k, (long long)m * k, (int)B, st);
+        if (wide) {
+            batch_transpose(ut, dvt, B, m, k, st);    // A's V^T (k x N) = (Q U_R)^T
+            batch_transpose(vtt, du, B, k, k, st);    // A's U (M x k) = V_R
+        }
+    }
+    check_converged(di, B, st, "svd");
+    call.finish();
+}
+
+}  // namespace
+
 // reference: src/svd.mm:1058-1106 (core::svd)
 void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
     require_gpu_allowed("svd");
@@ -147,9 +225,14 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
         }
         return;
     }
-    if (!svd_small_fits(M, N))
+    if (!svd_small_fits(M, N)) {
+        if (K <= 64 && qr_blocked_fits(std::max(M, N), K)) {
+            svd_tall(a, u, s, vt, info);
+            return;
+        }
         invalid("[svd] " + std::to_string(M) + "x" + std::to_string(N) +
-                ": this build's SVD kernels take min(M, N) <= 64 and max(M, N) <= 128 so far");
+                ": this build's SVD kernels take min(M, N) <= 64 and max(M, N) <= 4096 so far");
+    }
     Call call;
     const float* da = call.in(a.data, (size_t)B * M * N);
     float* ds = call.out(s, (size_t)B * K);

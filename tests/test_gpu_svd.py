@@ -116,3 +116,46 @@ def test_host_and_device_pointers_agree(cuda, api):
     u1, s1, vt1, _ = api.svd(a, True)
     u2, s2, vt2, _ = api.svd(dev(torch, a), True)
     assert np.array_equal(s1, to_np(s2)) and np.array_equal(u1, to_np(u2)) and np.array_equal(vt1, to_np(vt2))
+
+
+# ---- beyond the batched kernel's 128 rows: QR, then the SVD of R ----
+
+@pytest.mark.parametrize("m,n,batch", [(129, 64, 6), (300, 40, 5), (1000, 64, 3), (4096, 16, 2), (40, 300, 5),
+                                       (64, 1000, 2), (2000, 1, 3)])
+def test_tall_and_wide(cuda, api, oracle, m, n, batch):
+    a = gaussian((batch, m, n), seed=m * 7 + n)
+    u, s, vt, info = api.svd(a, True)
+    uo, so, vto, io = oracle.svd(a, True)
+    info = u32(info)
+    assert np.all((info >> 16) & 1) and not np.any((info >> 17) & 1)
+    recon, ou, ov = svd_residuals(a, u, s, vt)
+    close = values_close(s, so)
+    k = min(m, n)
+    print(f"[svd {m}x{n}] recon {recon.max():.3e} orthoU {ou.max():.3e} orthoV {ov.max():.3e} values {close.max():.3e}")
+    assert u.shape == (batch, m, k) and vt.shape == (batch, k, n)
+    assert recon.max() <= bound(max(m, n)) and ou.max() <= bound(k) and ov.max() <= bound(k)
+    assert close.max() <= 1e-5
+    assert np.all(np.diff(s, axis=-1) <= 0) and np.all(s >= 0)
+    _, s2, _, _ = api.svd(a, False)
+    assert values_close(s2, s).max() <= 1e-6
+
+
+def test_tall_special(cuda, api, oracle):
+    rng = np.random.default_rng(41)
+    m, n = 700, 48
+    mats = [np.zeros((m, n), np.float32), rng.standard_normal((m, n)).astype(np.float32),
+            (rng.standard_normal((m, 8)) @ rng.standard_normal((8, n))).astype(np.float32),   # rank 8
+            (rng.standard_normal((m, n)) * 1e30).astype(np.float32)]
+    a = np.stack(mats)
+    a[1, 5, 7] = np.nan
+    u, s, vt, info = api.svd(a, True)
+    info = u32(info)
+    assert np.isnan(s[1]).all() and np.isnan(u[1]).all() and np.isnan(vt[1]).all() and info[1] == (1 << 17)
+    ok = [0, 2, 3]
+    assert not np.isnan(s[ok]).any() and not np.isnan(u[ok]).any()
+    _, so, _, _ = oracle.svd(a[ok], True)
+    recon, ou, ov = svd_residuals(a[ok], u[ok], s[ok], vt[ok])
+    recon[0] = 0.0   # zero matrix: nothing to reconstruct
+    assert recon.max() <= bound(m) and ou.max() <= bound(n) and ov.max() <= bound(n)
+    assert values_close(s[ok], so).max() <= 1e-5
+    assert (info[2] >> 18) & 1   # rank-deficient
