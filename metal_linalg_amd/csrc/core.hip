@@ -230,8 +230,22 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
             svd_tall(a, u, s, vt, info);
             return;
         }
-        invalid("[svd] " + std::to_string(M) + "x" + std::to_string(N) +
-                ": this build's SVD kernels take min(M, N) <= 64 and max(M, N) <= 4096 so far");
+        if (!svd_large_fits(M, N))
+            invalid("[svd] " + std::to_string(M) + "x" + std::to_string(N) +
+                    ": this build's SVD kernels take max(M, N) <= 4096");
+        Call call;
+        const size_t per = (size_t)M * N;
+        const float* da = call.in(a.data, (size_t)B * per);
+        float* ds = call.out(s, (size_t)B * K);
+        float* du = u ? call.out(u, (size_t)B * M * K) : nullptr;
+        float* dvt = vt ? call.out(vt, (size_t)B * K * N) : nullptr;
+        uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+        float* work = static_cast<float*>(call.scratch(svd_large_workspace(M, N)));
+        for (uint32_t b = 0; b < B; ++b)
+            svd_large_one(da + b * per, du ? du + (size_t)b * M * K : nullptr, ds + (size_t)b * K,
+                          dvt ? dvt + (size_t)b * K * N : nullptr, di + b, work, M, N, call.stream());
+        call.finish();
+        return;
     }
     Call call;
     const float* da = call.in(a.data, (size_t)B * M * N);

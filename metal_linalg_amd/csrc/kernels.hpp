@@ -80,6 +80,13 @@ size_t eigh_tridiag_floats(uint32_t n);
 void eigh_tridiag_one(const EighWork& w, uint32_t n, float* w_out, float* v_out, uint32_t* info, hipStream_t s);
 
 // ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128 ----
+// One m x n matrix with min(m, n) > 64 (max(m, n) <= 4096), through the
+// large eigh path on [0 A^T; A 0]; work = svd_large_workspace(m, n) bytes.
+bool svd_large_fits(uint32_t m, uint32_t n);
+size_t svd_large_workspace(uint32_t m, uint32_t n);
+void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info, float* work, uint32_t m,
+                   uint32_t n, hipStream_t st);
+
 bool svd_small_fits(uint32_t m, uint32_t n);
 size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes
 void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, float* ws, uint32_t batch, uint32_t m,

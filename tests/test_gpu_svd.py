@@ -159,3 +159,54 @@ def test_tall_special(cuda, api, oracle):
     assert recon.max() <= bound(m) and ou.max() <= bound(n) and ov.max() <= bound(n)
     assert values_close(s[ok], so).max() <= 1e-5
     assert (info[2] >> 18) & 1   # rank-deficient
+
+
+# ---- min(M, N) > 64: the large eigh path on [0 A^T; A 0] ----
+
+@pytest.mark.parametrize("m,n", [(65, 65), (100, 80), (80, 100), (300, 130), (130, 513), (1024, 1024)])
+def test_large(cuda, api, oracle, m, n):
+    a = gaussian((1, m, n), seed=m * 3 + n)
+    u, s, vt, info = api.svd(a, True)
+    uo, so, vto, io = oracle.svd(a, True)
+    info = u32(info)
+    k = min(m, n)
+    assert info[0] & (1 << 16) and not info[0] & (1 << 17)
+    recon, ou, ov = svd_residuals(a, u, s, vt)
+    close = values_close(s, so)
+    print(f"[svd large {m}x{n}] recon {recon.max():.3e} orthoU {ou.max():.3e} orthoV {ov.max():.3e} "
+          f"values {close.max():.3e} bound {bound(max(m, n)):.3e}")
+    assert u.shape == (1, m, k) and vt.shape == (1, k, n)
+    assert recon.max() <= bound(max(m, n)) and ou.max() <= bound(k) and ov.max() <= bound(k)
+    assert close.max() <= 1e-5
+    assert np.all(np.diff(s, axis=-1) <= 0) and np.all(s >= 0)
+    _, s2, _, _ = api.svd(a, False)
+    assert values_close(s2, s).max() <= 1e-5
+
+
+def test_large_special(cuda, api, oracle):
+    rng = np.random.default_rng(43)
+    m, n = 300, 200
+    cases = {
+        "rank 50": (rng.standard_normal((m, 50)) @ rng.standard_normal((50, n))).astype(np.float32),
+        "zero": np.zeros((m, n), np.float32),
+        "graded": ((rng.standard_normal((m, n)) * 10.0 ** np.linspace(0, -6, n)[None, :])).astype(np.float32),
+        "1e30": (rng.standard_normal((m, n)) * 1e30).astype(np.float32),
+    }
+    for name, x in cases.items():
+        a = x[None]
+        u, s, vt, info = api.svd(a, True)
+        info = u32(info)
+        _, so, _, _ = oracle.svd(a, True)
+        recon, ou, ov = svd_residuals(a, u, s, vt)
+        if name == "zero":
+            recon[:] = 0.0
+        print(f"[svd large {name}] recon {recon.max():.3e} orthoU {ou.max():.3e} orthoV {ov.max():.3e} "
+              f"values {values_close(s, so).max():.3e} info {info[0]:#x}")
+        assert recon.max() <= bound(m) and ou.max() <= bound(n) and ov.max() <= bound(n)
+        assert values_close(s, so).max() <= 1e-5
+        if name in ("rank 50", "zero"):
+            assert info[0] & (1 << 18)
+    a = rng.standard_normal((1, m, n)).astype(np.float32)
+    a[0, 3, 4] = np.inf
+    u, s, vt, info = api.svd(a, True)
+    assert np.isnan(s).all() and np.isnan(u).all() and np.isnan(vt).all() and u32(info)[0] == (1 << 17)
