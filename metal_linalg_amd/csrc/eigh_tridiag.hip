@@ -244,12 +244,15 @@ __global__ __launch_bounds__(256) void newton_schulz_kernel(float* __restrict__ 
 }
 
 // T (nb x nb, upper, row-major) of the compact WY form of nb reflectors
-// from S = V^T V (nb x nb) and tau: T[k][k] = tau_k,
-// T[0:k, k] = -tau_k T[0:k, 0:k] S[0:k, k].  One workgroup of 64 threads.
+// from S = V^T V (nb x nb, symmetric) and tau: T[k][k] = tau_k,
+// T[0:k, k] = -tau_k T[0:k, 0:k] S[0:k, k].  Row t of T depends only on row
+// t's earlier entries and on S, so each of the 64 threads builds its own row
+// in registers (every index compile-time, no barrier between columns),
+// reading S's rows (= columns) as float4 broadcasts from LDS.
 __global__ __launch_bounds__(64) void wy_t_kernel(const float* __restrict__ S, const float* __restrict__ tau, int nb,
                                                   float* __restrict__ T) {
-    __shared__ float Ts[NBT][NBT + 1];
-    __shared__ float Ss[NBT][NBT + 1];
+    __shared__ float Ss[NBT][NBT + 4];
+    __shared__ float ts[NBT];
     const int t = threadIdx.x;
     for (int i0 = 0; i0 < NBT; i0 += 16) {
         float x[16];
@@ -261,23 +264,30 @@ __global__ __launch_bounds__(64) void wy_t_kernel(const float* __restrict__ S, c
             x[u] = in ? x[u] : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            Ss[i0 + u][t] = x[u];
-            Ts[i0 + u][t] = 0.0f;
-        }
+        for (int u = 0; u < 16; ++u) Ss[i0 + u][t] = x[u];
     }
+    ts[t] = t < nb ? tau[t] : 0.0f;
     __syncthreads();
-    for (int k = 0; k < nb; ++k) {
-        const float tk = tau[k];
-        float s = 0.0f;
-        if (t < k)
-            for (int l = t; l < k; ++l) s = fmaf(Ts[t][l], Ss[l][k], s);
-        __syncthreads();
-        if (t < k) Ts[t][k] = -tk * s;
-        if (t == k) Ts[k][k] = tk;
-        __syncthreads();
+    float tr[NBT];   // row t of T; entries left of the diagonal stay 0
+#pragma unroll
+    for (int k = 0; k < NBT; ++k) {
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int l0 = 0; l0 < k; l0 += 4) {
+            const float4 sv = *reinterpret_cast<const float4*>(&Ss[k][l0]);
+            s0 = fmaf(tr[l0], sv.x, s0);
+            if (l0 + 1 < k) s1 = fmaf(tr[l0 + 1], sv.y, s1);
+            if (l0 + 2 < k) s2 = fmaf(tr[l0 + 2], sv.z, s2);
+            if (l0 + 3 < k) s3 = fmaf(tr[l0 + 3], sv.w, s3);
+        }
+        const float tk = ts[k];
+        tr[k] = t < k ? -tk * ((s0 + s1) + (s2 + s3)) : (t == k ? tk : 0.0f);
     }
-    for (int idx = t; idx < nb * nb; idx += 64) T[idx] = Ts[idx / nb][idx % nb];
+    if (t < nb) {
+#pragma unroll
+        for (int k = 0; k < NBT; ++k)
+            if (k < nb) T[t * nb + k] = tr[k];
+    }
 }
 
 // out[i][j] = Z[i][perm[j]]; w[j] = lam[perm[j]] 2^e
