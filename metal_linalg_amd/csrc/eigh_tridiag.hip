@@ -100,13 +100,13 @@ struct Cluster {         // consecutive slots of one block, close together
 // One thread per cluster.  Z[r * ldz + slot] holds the vectors (rows of
 // the block; the thread also zeroes the rest of its columns).  U is scratch
 // for the factor: 3 floats per row, [3 * row][thread] (coalesced).
-__global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __restrict__ d,
+__global__ __launch_bounds__(64) void inverse_iteration_kernel(const float* __restrict__ d,
                                                                 const float* __restrict__ e,
                                                                 const Cluster* __restrict__ cl, int ncl,
                                                                 const float* __restrict__ lam, float tnorm,
                                                                 float* __restrict__ Z, int ldz, int n,
                                                                 float* __restrict__ U) {
-    const int tid = blockIdx.x * 256 + threadIdx.x;
+    const int tid = blockIdx.x * 64 + threadIdx.x;
     if (tid >= ncl) return;
     const Cluster c = cl[tid];
     const int s = c.start, m = c.size;
@@ -132,16 +132,23 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
             float a = d[s] - lambda;         // the running diagonal entry of row k
             float cc = e[s];                 // row k's superdiagonal
             float b0 = z[(size_t)s * ldz];   // the running right-hand side of row k
-            for (int k0 = 0; k0 < m - 1; k0 += CH) {
-                float zb[CH], db[CH], eb[CH], en[CH];
+            // chunk loads run one chunk ahead of the recurrence (the next
+            // chunk's rows are never the ones this chunk writes)
+            float zb[CH], db[CH], eb[CH], en[CH];
+            auto load_fwd = [&](int k0, float (&zl)[CH], float (&dl)[CH], float (&el)[CH], float (&nl)[CH]) {
 #pragma unroll
-                for (int c = 0; c < CH; ++c) {
-                    const int k = min(k0 + c, m - 2);
-                    zb[c] = z[(size_t)(s + k + 1) * ldz];
-                    db[c] = d[s + k + 1];
-                    eb[c] = e[s + k];
-                    en[c] = k + 1 < m - 1 ? e[s + k + 1] : 0.0f;
+                for (int j = 0; j < CH; ++j) {
+                    const int k = min(k0 + j, m - 2);
+                    zl[j] = z[(size_t)(s + k + 1) * ldz];
+                    dl[j] = d[s + k + 1];
+                    el[j] = e[s + k];
+                    nl[j] = k + 1 < m - 1 ? e[s + k + 1] : 0.0f;
                 }
+            };
+            load_fwd(0, zb, db, eb, en);
+            for (int k0 = 0; k0 < m - 1; k0 += CH) {
+                float zn[CH], dn[CH], ebn[CH], enn[CH];
+                load_fwd(k0 + CH < m - 1 ? k0 + CH : k0, zn, dn, ebn, enn);
 #pragma unroll
                 for (int c = 0; c < CH; ++c) {
                     const int k = k0 + c;
@@ -150,28 +157,19 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
                     const float an = db[c] - lambda;
                     const float cn = en[c];
                     const float b1 = zb[c];
-                    float p0, p1, p2, nb0, na, nc, rhs;
-                    if (fabsf(a) >= fabsf(bk)) {
-                        const float l = a == 0.0f ? 0.0f : bk * __builtin_amdgcn_rcpf(a);
-                        p0 = a;
-                        p1 = cc;
-                        p2 = 0.0f;
-                        rhs = b0;
-                        na = an - l * cc;
-                        nc = cn;
-                        nb0 = b1 - l * b0;
-                    } else {
-                        const float l = a * __builtin_amdgcn_rcpf(bk);
-                        p0 = bk;
-                        p1 = an;
-                        p2 = cn;
-                        rhs = b1;
-                        na = cc - l * an;
-                        nc = -l * cn;
-                        nb0 = b0 - l * b1;
-                    }
-                    if (p0 == 0.0f) p0 = tol;
-                    u0[(3 * (size_t)k + 0) * us] = __builtin_amdgcn_rcpf(p0);   // the backward pass multiplies
+                    const bool keep = fabsf(a) >= fabsf(bk);
+                    float p0 = keep ? a : bk;
+                    // pivots below tol (zero, or subnormal) become +-tol
+                    p0 = fabsf(p0) < tol ? copysignf(tol, p0) : p0;
+                    const float r0 = __builtin_amdgcn_rcpf(p0);
+                    const float l = (keep ? bk : a) * r0;
+                    const float p1 = keep ? cc : an;
+                    const float p2 = keep ? 0.0f : cn;
+                    const float rhs = keep ? b0 : b1;
+                    const float na = keep ? fmaf(-l, cc, an) : fmaf(-l, an, cc);
+                    const float nc = keep ? cn : -l * cn;
+                    const float nb0 = keep ? fmaf(-l, b0, b1) : fmaf(-l, b1, b0);
+                    u0[(3 * (size_t)k + 0) * us] = r0;   // the backward pass multiplies
                     u0[(3 * (size_t)k + 1) * us] = p1;
                     u0[(3 * (size_t)k + 2) * us] = p2;
                     z[(size_t)(s + k) * ldz] = rhs;
@@ -179,8 +177,15 @@ __global__ __launch_bounds__(256) void inverse_iteration_kernel(const float* __r
                     cc = nc;
                     b0 = nb0;
                 }
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    zb[c] = zn[c];
+                    db[c] = dn[c];
+                    eb[c] = ebn[c];
+                    en[c] = enn[c];
+                }
             }
-            if (a == 0.0f) a = tol;
+            a = fabsf(a) < tol ? copysignf(tol, a) : a;
             // backward: U x = rhs, and |x|^2, in chunks from the bottom
             float x2 = 0.0f, x1 = 0.0f, nrm = 0.0f;
             {
@@ -475,7 +480,7 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
     float* U = scratch;
     {
         KernelTimer tm("tridiag_vectors", s);
-        hipLaunchKernelGGL(inverse_iteration_kernel, dim3((unsigned)cdiv(ncl, 256)), dim3(256), 0, s, w.d, dE,
+        hipLaunchKernelGGL(inverse_iteration_kernel, dim3((unsigned)cdiv(ncl, 64)), dim3(64), 0, s, w.d, dE,
                            clusters, ncl, lam, tnorm, Z, n, n, U);
         // Z <- Z (3 I - Z^T Z) / 2
         float* G = scratch;
