@@ -59,11 +59,29 @@ struct SvdWs {
 };
 
 // ---------------------------------------------------------------- bidiag
+constexpr int kChunks = kMaxM / 4;   // 4-row chunks of a lane's column
+
+struct BidiagLds {
+    float v[kMaxM];       // the left reflector: 0 above row k, 1 at row k
+    float w[kMaxM];       // A u for the right reflector u
+    float p[64][68];      // products x_c[r] u_c of one half of the rows, [c][r]
+};
+
+// Lane c holds column c of the problem in VGPRs (rows >= M and columns >= N
+// zero, which every reflector leaves zero).  Step k: lane k publishes its
+// column; the norm comes from a wave sum; the reflector goes back to LDS and
+// every lane forms v^T x_c and its update from 16-byte broadcasts.  The
+// right reflector is row k (element k of every lane's column, read by a
+// wave-uniform select), its norm a wave sum; A u is a transposed reduction
+// through LDS (lanes store x_c[r] u_c for 64 rows, then lane t sums row t),
+// and the update again reads A u as broadcasts.  Row chunks above row k are
+// skipped by wave-uniform branches; the rows above k that a chunk still
+// covers are finished and never read with a non-zero coefficient.
 __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict__ A, float* __restrict__ ws,
                                                         uint32_t batch, uint32_t rows, uint32_t cols, int trans,
                                                         int vectors) {
-    __shared__ float a[kMaxM][kPitch];
-    const int t = threadIdx.x;
+    __shared__ __align__(16) BidiagLds s;
+    const int c = threadIdx.x;
     const size_t mat = blockIdx.x;
     if (mat >= batch) return;   // whole wave: uniform
     const int M = trans ? (int)cols : (int)rows;
@@ -72,93 +90,154 @@ __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict_
     float* w = ws + mat * W.per();
     const float* src = A + mat * (size_t)rows * cols;
 
-    // load (transposed for a wide input), scan
-    float amax = 0.0f;
-    int bad = 0;
-    for (int r = 0; r < M; ++r) {
-        if (t < N) {
-            const float v = trans ? src[(size_t)t * cols + r] : src[(size_t)r * cols + t];
-            amax = fmaxf(amax, fabsf(v));
-            bad |= !finite_f(v);
-            a[r][t] = v;
-        }
+    // load (transposed for a wide input) with clamped indices, scan
+    float x[kMaxM];
+    const int cc = c < N ? c : N - 1;
+#pragma unroll
+    for (int r = 0; r < kMaxM; ++r) {
+        const int rr = r < M ? r : M - 1;
+        const float v = trans ? src[(size_t)cc * cols + rr] : src[(size_t)rr * cols + cc];
+        x[r] = (r < M && c < N) ? v : 0.0f;
+    }
+    float amax = 0.0f, chk = 0.0f;   // chk becomes NaN at a NaN or an infinity
+#pragma unroll
+    for (int r = 0; r < kMaxM; ++r) {
+        amax = fmaxf(amax, fabsf(x[r]));
+        chk = fmaf(x[r], 0.0f, chk);
     }
     amax = group_max<64>(amax);
-    bad = group_or<64>(bad);
+    const int bad = group_or<64>(chk != chk ? 1 : 0);
     const int ex = bad ? 0 : scale_exponent(amax);
-    for (int r = 0; r < M; ++r)
-        if (t < N) a[r][t] = bad ? 0.0f : ldexpf(a[r][t], -ex);
-    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < kMaxM; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -ex);
 
     for (int k = 0; k < N; ++k) {
+        const int j0 = k >> 2;   // the chunk holding row k
         // ---- left reflector on column k, rows k.. ----
-        float part = 0.0f;
-        for (int r = k + 1 + t; r < M; r += 64) part = fmaf(a[r][k], a[r][k], part);
-        const float ss = group_sum<64>(part);
-        const float alpha = a[k][k];
+        if (c == k) {
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j)
+                if (j >= j0)
+                    *reinterpret_cast<float4*>(&s.v[4 * j]) = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2],
+                                                                          x[4 * j + 3]);
+        }
+        __syncthreads();
+        const float a0 = s.v[c], a1 = s.v[c + 64];   // rows c and c + 64 (> k)
+        const float alpha = s.v[k];
+        const float l0 = c > k ? a0 : 0.0f;
+        const float ss = wave_sum_f(fmaf(l0, l0, a1 * a1));
         float beta = alpha, tau = 0.0f, scale = 1.0f;
         if (ss >= kTinySumsq) {
             beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
             tau = (beta - alpha) / beta;
             scale = 1.0f / (alpha - beta);
         }
-        wave_lds_sync();
-        for (int r = k + 1 + t; r < M; r += 64) a[r][k] *= scale;
-        wave_lds_sync();
-        if (t > k && t < N && tau != 0.0f) {
-            float dot = a[k][t];
-            for (int r = k + 1; r < M; ++r) dot = fmaf(a[r][k], a[r][t], dot);
-            dot *= tau;
-            a[k][t] -= dot;
-            for (int r = k + 1; r < M; ++r) a[r][t] = fmaf(-dot, a[r][k], a[r][t]);
+        __syncthreads();   // every read of column k before the reflector replaces it
+        const float v0 = c < k ? 0.0f : (c == k ? 1.0f : a0 * scale);
+        const float v1 = a1 * scale;
+        s.v[c] = v0;
+        s.v[c + 64] = v1;
+        if (vectors) {   // v_k, contiguous
+            if (c < M) w[W.refl() + (size_t)k * M + c] = v0;
+            if (c + 64 < M) w[W.refl() + (size_t)k * M + c + 64] = v1;
         }
-        if (t == 0) {
+        if (c == 0) {
             w[W.d() + k] = beta;
             w[W.tq() + k] = tau;
         }
-        if (vectors) {   // v_k, contiguous: [k] = 1, below from the column
-            for (int r = t; r < M; r += 64)
-                w[W.refl() + (size_t)k * M + r] = r < k ? 0.0f : (r == k ? 1.0f : a[r][k]);
+        __syncthreads();
+        if (tau != 0.0f) {   // uniform
+            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                if (j >= j0) {
+                    const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
+                    d0 = fmaf(vv.x, x[4 * j], d0);
+                    d1 = fmaf(vv.y, x[4 * j + 1], d1);
+                    d2 = fmaf(vv.z, x[4 * j + 2], d2);
+                    d3 = fmaf(vv.w, x[4 * j + 3], d3);
+                }
+            }
+            const float g = c > k ? tau * ((d0 + d1) + (d2 + d3)) : 0.0f;
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                if (j >= j0) {
+                    const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
+                    x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
+                    x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
+                    x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
+                    x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+                }
+            }
         }
-        wave_lds_sync();
         if (k + 1 >= N) break;
         // ---- right reflector on row k, columns k+1.. ----
-        const float x = (t > k + 1 && t < N) ? a[k][t] : 0.0f;
-        const float ssr = group_sum<64>(x * x);
-        const float alr = a[k][k + 1];
+        float xk = 0.0f;   // element k of this lane's column (k < 64)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (j == j0) {
+                const int q = k & 3;
+                xk = q == 0 ? x[4 * j] : (q == 1 ? x[4 * j + 1] : (q == 2 ? x[4 * j + 2] : x[4 * j + 3]));
+            }
+        }
+        const float alr = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xk), k + 1));
+        const float ur = c > k + 1 ? xk : 0.0f;
+        const float ssr = wave_sum_f(ur * ur);
         float br = alr, taur = 0.0f, scr = 1.0f;
         if (ssr >= kTinySumsq) {
             br = -copysignf(sqrtf(fmaf(alr, alr, ssr)), alr);
             taur = (br - alr) / br;
             scr = 1.0f / (alr - br);
         }
-        wave_lds_sync();
-        if (t > k + 1 && t < N) a[k][t] *= scr;
-        wave_lds_sync();
-        if (taur != 0.0f) {
-            for (int r = k + 1 + t; r < M; r += 64) {
-                float dot = a[r][k + 1];
-                for (int c = k + 2; c < N; ++c) dot = fmaf(a[r][c], a[k][c], dot);
-                dot *= taur;
-                a[r][k + 1] -= dot;
-                for (int c = k + 2; c < N; ++c) a[r][c] = fmaf(-dot, a[k][c], a[r][c]);
-            }
-        }
-        if (t == 0) {
+        const float up = c == k + 1 ? 1.0f : ur * scr;   // u_c, 0 for c <= k
+        if (vectors && c < N) w[W.refr() + (size_t)k * N + c] = up;
+        if (c == 0) {
             w[W.e() + k] = br;
             w[W.tp() + k] = taur;
         }
-        if (vectors && t < N)   // u_k: [k+1] = 1, then the row
-            w[W.refr() + (size_t)k * N + t] = t <= k ? 0.0f : (t == k + 1 ? 1.0f : a[k][t]);
-        wave_lds_sync();
+        if (taur != 0.0f) {   // uniform
+            // A u, 64 rows at a time
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (h == 1 && M <= 64) break;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int r = 64 * h + 4 * j;
+                    *reinterpret_cast<float4*>(&s.p[c][4 * j]) =
+                        make_float4(x[r] * up, x[r + 1] * up, x[r + 2] * up, x[r + 3] * up);
+                }
+                __syncthreads();
+                float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int g8 = 0; g8 < 8; ++g8) {
+                    if (8 * g8 + 7 > k) {   // columns <= k have u = 0
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) acc[q] += s.p[8 * g8 + q][c];
+                    }
+                }
+                s.w[64 * h + c] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+                __syncthreads();
+            }
+            const float gr = taur * up;
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                if (j >= j0 && 4 * j < M) {
+                    const float4 ww = *reinterpret_cast<const float4*>(&s.w[4 * j]);
+                    x[4 * j] = fmaf(-gr, ww.x, x[4 * j]);
+                    x[4 * j + 1] = fmaf(-gr, ww.y, x[4 * j + 1]);
+                    x[4 * j + 2] = fmaf(-gr, ww.z, x[4 * j + 2]);
+                    x[4 * j + 3] = fmaf(-gr, ww.w, x[4 * j + 3]);
+                }
+            }
+        }
     }
-    if (t == 0) {
+    if (c == 0) {
         w[W.e() + N - 1] = 0.0f;
         w[W.tp() + N - 1] = 0.0f;
         w[W.meta()] = __int_as_float(ex);
         w[W.meta() + 1] = __int_as_float(bad);
     }
-    if (vectors && t < N) w[W.refr() + (size_t)(N - 1) * N + t] = 0.0f;
+    if (vectors && c < N) w[W.refr() + (size_t)(N - 1) * N + c] = 0.0f;
 }
 
 // ---------------------------------------------------------------- bdsqr
@@ -209,30 +288,27 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
     const int ex = __float_as_int(w[W.meta()]);
     const int bad = __float_as_int(w[W.meta() + 1]);
 
-    float qq[NN], ee[NN];
+    // q and e live in LDS only (every lane reads the same entries); the
+    // VGPRs hold this lane's rows of U_B and V_B
     float xu[VEC ? NN : 1], xv[VEC ? NN : 1];
+    if (VEC) {
 #pragma unroll
-    for (int i = 0; i < NN; ++i) {
-        qq[i] = i < n ? w[W.d() + i] : 0.0f;
-        ee[i] = (i >= 1 && i < n) ? w[W.e() + i - 1] : 0.0f;
-        if (VEC) {
+        for (int i = 0; i < NN; ++i) {
             xu[i] = i == lane ? 1.0f : 0.0f;
             xv[i] = i == lane ? 1.0f : 0.0f;
         }
     }
-    float anorm = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NN; ++i) anorm = fmaxf(anorm, fabsf(qq[i]) + fabsf(ee[i]));
-    if (lane < n) {
-        float qv = 0.0f, ev = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NN; ++i) {
-            qv = i == lane ? qq[i] : qv;
-            ev = i == lane ? ee[i] : ev;
-        }
+    {
+        const float qv = lane < n ? w[W.d() + (lane < n ? lane : 0)] : 0.0f;
+        const float ev = (lane >= 1 && lane < n) ? w[W.e() + (lane >= 1 ? lane - 1 : 0)] : 0.0f;
         s.q[lane] = qv;
         s.e[lane] = ev;
+        if (lane == 0) {
+            s.q[NN] = 0.0f;
+            s.e[NN] = 0.0f;
+        }
     }
+    const float anorm = group_max<64>(fabsf(s.q[lane]) + fabsf(s.e[lane]));
     wave_lds_sync();
     const float tol = kEps * anorm;
 
@@ -247,31 +323,40 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
             const bool se = lane <= k && (lane == 0 || fabsf(ei) <= tol);
             const bool sq = lane <= k && lane >= 1 && fabsf(qm) <= tol;
             const uint64_t any = __ballot(se || sq);
-            const int l = 63 - __clzll((long long)any);
+            int l = 63 - __clzll((long long)any);
+            // opaque to the optimiser: otherwise every unrolled test j >= l
+            // becomes a 64-bit compare of the ballot with 2^j, and the 64
+            // constants stay live in VGPRs
+            asm volatile("" : "+s"(l));
             const bool cancel = !((__ballot(se) >> l) & 1ull);
             if (cancel) {
                 // e[l] is cancelled by rotations of rows (l-1, i), i = l..k
                 const int nm = l - 1;
                 float cc = 0.0f, sn = 1.0f;
                 float unm = 0.0f;
+                // xu[nm] by wave-uniform branches (the asm keeps them branches:
+                // selects here would hold 64 lane masks live across the loop)
                 if (VEC) {
 #pragma unroll
-                    for (int j = 0; j < NN; ++j) unm = j == nm ? xu[j] : unm;
+                    for (int j = 0; j < NN; ++j)
+                        if (j == nm) {
+                            asm volatile("");
+                            unm = xu[j];
+                        }
                 }
                 bool done = false;
 #pragma unroll
                 for (int i = 0; i < NN; ++i) {
                     if (i >= l && i <= k && !done) {
-                        const float f = sn * ee[i];
-                        ee[i] = cc * ee[i];
-                        s.e[i] = ee[i];
+                        const float ei = s.e[i];
+                        const float f = sn * ei;
+                        s.e[i] = cc * ei;
                         if (fabsf(f) <= tol) {
                             done = true;
                         } else {
-                            const float g = qq[i];
+                            const float g = s.q[i];
                             float c2, s2;
                             const float h = rot(g, f, c2, s2);
-                            qq[i] = h;
                             s.q[i] = h;
                             cc = c2;
                             sn = -s2;
@@ -285,7 +370,11 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
                 }
                 if (VEC) {
 #pragma unroll
-                    for (int j = 0; j < NN; ++j) xu[j] = j == nm ? unm : xu[j];
+                    for (int j = 0; j < NN; ++j)
+                        if (j == nm) {
+                            asm volatile("");
+                            xu[j] = unm;
+                        }
                 }
                 wave_lds_sync();
             }
@@ -305,14 +394,13 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
             for (int j = 0; j < NN - 1; ++j) {
                 if (j >= l && j < k) {
                     const int i = j + 1;
-                    float g = ee[i];
-                    float y = qq[i];
+                    float g = s.e[i];
+                    float y = s.q[i];
                     float h = sn * g;
                     g = c * g;
                     float cz, sz;
                     const float z1 = rot(f, h, cz, sz);
-                    ee[j] = (j == l) ? 0.0f : z1;
-                    s.e[j] = ee[j];
+                    s.e[j] = z1;   // e[l] becomes 0 after the sweep
                     c = cz;
                     sn = sz;
                     f = fmaf(x, c, g * sn);
@@ -326,7 +414,6 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
                     }
                     float c2, s2;
                     const float z2 = rot(f, h, c2, s2);
-                    qq[j] = z2;
                     s.q[j] = z2;
                     if (z2 != 0.0f) {
                         c = c2;
@@ -339,32 +426,26 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
                         xu[j] = fmaf(uy, c, uz * sn);
                         xu[i] = fmaf(uz, c, -uy * sn);
                     }
-                    if (i == k) {
-                        ee[i] = f;
-                        qq[i] = x;
-                        s.e[i] = f;
-                        s.q[i] = x;
-                    }
                 }
             }
+            s.e[l] = 0.0f;
+            s.e[k] = f;
+            s.q[k] = x;
             wave_lds_sync();
         }
     }
 
     // signs: non-negative values, the matching V columns negated
-#pragma unroll
-    for (int j = 0; j < NN; ++j) {
-        if (j < n && qq[j] < 0.0f) {
-            qq[j] = -qq[j];
-            if (VEC) xv[j] = -xv[j];
-        }
-    }
     wave_lds_sync();
-    if (lane < n) {
-        float qv = 0.0f;
+    {
+        const float qv = s.q[lane];
+        const uint64_t neg = __ballot(lane < n && qv < 0.0f);
+        if (VEC) {
 #pragma unroll
-        for (int i = 0; i < NN; ++i) qv = i == lane ? qq[i] : qv;
-        s.q[lane] = qv;
+            for (int j = 0; j < NN; ++j) xv[j] = ((neg >> j) & 1ull) ? -xv[j] : xv[j];
+        }
+        wave_lds_sync();
+        if (lane < n) s.q[lane] = fabsf(qv);
     }
     wave_lds_sync();
     float smax = 0.0f, smin = 3.0e38f;
@@ -415,9 +496,14 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
 }
 
 // ---------------------------------------------------------- back-transform
+// Lane c holds column c of U_B (then V_B) in VGPRs.  Reflector k is loaded
+// by the wave (two rows per lane) one step ahead, staged in one of two LDS
+// buffers, and read back as 16-byte broadcasts; chunks above the
+// reflector's first non-zero row are skipped (wave-uniform).
 __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __restrict__ ws, float* __restrict__ U,
                                                                float* __restrict__ Vt, uint32_t batch, uint32_t rows,
                                                                uint32_t cols, int trans) {
+    __shared__ __align__(16) float vb[2][kMaxM];
     __shared__ float tr[kMaxN][kMaxN + 1];
     const int c = threadIdx.x;
     const size_t mat = blockIdx.x;
@@ -428,40 +514,107 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
     const float* w = ws + mat * W.per();
     const int bad = __float_as_int(w[W.meta() + 1]);
     const float nanv = qnan();
+    const int cc = c < N ? c : N - 1;
 
-    // U_p = H_0 ... H_{N-1} [U_B; 0], lane c its column c
+    // U_p = H_0 ... H_{N-1} [U_B; 0]
     float x[kMaxM];
 #pragma unroll
-    for (int r = 0; r < kMaxM; ++r) x[r] = (c < N && r < N) ? w[W.ub() + (size_t)r * N + c] : 0.0f;
-    for (int k = N - 1; k >= 0; --k) {
-        const float tau = w[W.tq() + k];
-        if (tau == 0.0f) continue;   // uniform
-        const float* v = w + W.refl() + (size_t)k * M;
-        float d = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kMaxM; ++r)
-            if (r < M) d = fmaf(v[r], x[r], d);   // v[r] = 0 above k
-        d *= tau;
-#pragma unroll
-        for (int r = 0; r < kMaxM; ++r)
-            if (r < M) x[r] = fmaf(-d, v[r], x[r]);
+    for (int r = 0; r < kMaxN; ++r) {
+        const float v = w[W.ub() + (size_t)(r < N ? r : N - 1) * N + cc];
+        x[r] = (c < N && r < N) ? v : 0.0f;
     }
-    // V_p = G_0 ... G_{N-2} V_B, lane c its column c
+#pragma unroll
+    for (int r = kMaxN; r < kMaxM; ++r) x[r] = 0.0f;
+    {
+        const int c1 = c + 64 < M ? c + 64 : M - 1;
+        float n0 = 0.0f, n1 = 0.0f, tn = 0.0f;
+        auto fetch = [&](int k) {
+            const float* v = w + W.refl() + (size_t)k * M;
+            const float p0 = v[c < M ? c : M - 1], p1 = v[c1];
+            n0 = c < M ? p0 : 0.0f;
+            n1 = c + 64 < M ? p1 : 0.0f;
+            tn = w[W.tq() + k];
+        };
+        fetch(N - 1);
+        for (int k = N - 1; k >= 0; --k) {
+            float* vk = vb[k & 1];
+            vk[c] = n0;
+            vk[c + 64] = n1;
+            const float tau = tn;
+            if (k > 0) fetch(k - 1);
+            __syncthreads();
+            if (tau == 0.0f) continue;   // uniform
+            const int j0 = k >> 2;       // v_k is zero above row k
+            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                if (j >= j0 && 4 * j < M) {
+                    const float4 vv = *reinterpret_cast<const float4*>(&vk[4 * j]);
+                    d0 = fmaf(vv.x, x[4 * j], d0);
+                    d1 = fmaf(vv.y, x[4 * j + 1], d1);
+                    d2 = fmaf(vv.z, x[4 * j + 2], d2);
+                    d3 = fmaf(vv.w, x[4 * j + 3], d3);
+                }
+            }
+            const float g = tau * ((d0 + d1) + (d2 + d3));
+#pragma unroll
+            for (int j = 0; j < kChunks; ++j) {
+                if (j >= j0 && 4 * j < M) {
+                    const float4 vv = *reinterpret_cast<const float4*>(&vk[4 * j]);
+                    x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
+                    x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
+                    x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
+                    x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+                }
+            }
+        }
+    }
+    // V_p = G_0 ... G_{N-2} V_B
     float y[kMaxN];
 #pragma unroll
-    for (int j = 0; j < kMaxN; ++j) y[j] = (c < N && j < N) ? w[W.vb() + (size_t)j * N + c] : 0.0f;
-    for (int k = N - 2; k >= 0; --k) {
-        const float tau = w[W.tp() + k];
-        if (tau == 0.0f) continue;
-        const float* u = w + W.refr() + (size_t)k * N;
-        float d = 0.0f;
+    for (int j = 0; j < kMaxN; ++j) {
+        const float v = w[W.vb() + (size_t)(j < N ? j : N - 1) * N + cc];
+        y[j] = (c < N && j < N) ? v : 0.0f;
+    }
+    __syncthreads();   // the last U reflector's reads before the buffers are reused
+    if (N >= 2) {
+        float n0 = 0.0f, tn = 0.0f;
+        auto fetch = [&](int k) {
+            n0 = c < N ? w[W.refr() + (size_t)k * N + cc] : 0.0f;
+            tn = w[W.tp() + k];
+        };
+        fetch(N - 2);
+        for (int k = N - 2; k >= 0; --k) {
+            float* uk = vb[k & 1];
+            uk[c] = n0;
+            const float tau = tn;
+            if (k > 0) fetch(k - 1);
+            __syncthreads();
+            if (tau == 0.0f) continue;
+            const int j0 = (k + 1) >> 2;   // u_k is zero above entry k + 1
+            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kMaxN; ++j)
-            if (j < N) d = fmaf(u[j], y[j], d);
-        d *= tau;
+            for (int j = 0; j < kMaxN / 4; ++j) {
+                if (j >= j0 && 4 * j < N) {
+                    const float4 uu = *reinterpret_cast<const float4*>(&uk[4 * j]);
+                    d0 = fmaf(uu.x, y[4 * j], d0);
+                    d1 = fmaf(uu.y, y[4 * j + 1], d1);
+                    d2 = fmaf(uu.z, y[4 * j + 2], d2);
+                    d3 = fmaf(uu.w, y[4 * j + 3], d3);
+                }
+            }
+            const float g = tau * ((d0 + d1) + (d2 + d3));
 #pragma unroll
-        for (int j = 0; j < kMaxN; ++j)
-            if (j < N) y[j] = fmaf(-d, u[j], y[j]);
+            for (int j = 0; j < kMaxN / 4; ++j) {
+                if (j >= j0 && 4 * j < N) {
+                    const float4 uu = *reinterpret_cast<const float4*>(&uk[4 * j]);
+                    y[4 * j] = fmaf(-g, uu.x, y[4 * j]);
+                    y[4 * j + 1] = fmaf(-g, uu.y, y[4 * j + 1]);
+                    y[4 * j + 2] = fmaf(-g, uu.z, y[4 * j + 2]);
+                    y[4 * j + 3] = fmaf(-g, uu.w, y[4 * j + 3]);
+                }
+            }
+        }
     }
     // outputs: tall: U = U_p (M x N), Vt = V_p^T (N x N).
     //          wide: U = V_p (rows x rows), Vt = U_p^T (rows x cols).
@@ -476,7 +629,7 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
 #pragma unroll
             for (int j = 0; j < kMaxN; ++j) tr[c][j] = y[j];
         }
-        wave_lds_sync();
+        __syncthreads();
         float* vo = Vt + mat * (size_t)N * N;
         if (c < N)
             for (int i = 0; i < N; ++i) vo[(size_t)i * N + c] = bad ? nanv : tr[i][c];
