@@ -149,24 +149,30 @@ __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict_
         if (tau != 0.0f) {   // uniform
             float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j >= j0) {
-                    const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
-                    d0 = fmaf(vv.x, x[4 * j], d0);
-                    d1 = fmaf(vv.y, x[4 * j + 1], d1);
-                    d2 = fmaf(vv.z, x[4 * j + 2], d2);
-                    d3 = fmaf(vv.w, x[4 * j + 3], d3);
+            for (int g8 = 0; g8 < kChunks / 8; ++g8) {
+                if (8 * g8 + 7 >= j0) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                    for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                        const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
+                        d0 = fmaf(vv.x, x[4 * j], d0);
+                        d1 = fmaf(vv.y, x[4 * j + 1], d1);
+                        d2 = fmaf(vv.z, x[4 * j + 2], d2);
+                        d3 = fmaf(vv.w, x[4 * j + 3], d3);
+                    }
                 }
             }
             const float g = c > k ? tau * ((d0 + d1) + (d2 + d3)) : 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j >= j0) {
-                    const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
-                    x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
-                    x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
-                    x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
-                    x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+            for (int g8 = 0; g8 < kChunks / 8; ++g8) {
+                if (8 * g8 + 7 >= j0) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                    for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                        const float4 vv = *reinterpret_cast<const float4*>(&s.v[4 * j]);
+                        x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
+                        x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
+                        x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
+                        x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+                    }
                 }
             }
         }
@@ -220,13 +226,16 @@ __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict_
             }
             const float gr = taur * up;
 #pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j >= j0 && 4 * j < M) {
-                    const float4 ww = *reinterpret_cast<const float4*>(&s.w[4 * j]);
-                    x[4 * j] = fmaf(-gr, ww.x, x[4 * j]);
-                    x[4 * j + 1] = fmaf(-gr, ww.y, x[4 * j + 1]);
-                    x[4 * j + 2] = fmaf(-gr, ww.z, x[4 * j + 2]);
-                    x[4 * j + 3] = fmaf(-gr, ww.w, x[4 * j + 3]);
+            for (int g8 = 0; g8 < kChunks / 8; ++g8) {
+                if (8 * g8 + 7 >= j0 && 32 * g8 < M) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                    for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                        const float4 ww = *reinterpret_cast<const float4*>(&s.w[4 * j]);
+                        x[4 * j] = fmaf(-gr, ww.x, x[4 * j]);
+                        x[4 * j + 1] = fmaf(-gr, ww.y, x[4 * j + 1]);
+                        x[4 * j + 2] = fmaf(-gr, ww.z, x[4 * j + 2]);
+                        x[4 * j + 3] = fmaf(-gr, ww.w, x[4 * j + 3]);
+                    }
                 }
             }
         }
@@ -248,29 +257,23 @@ struct BdLds {
     int perm[kMaxN];
 };
 
-// (c, s, r) of the rotation taking (f, h) to (r, 0), robust to tiny pairs
-// (rescaled by a power of two so that f^2 + h^2 is never subnormal).
+// (c, s, r) of the rotation taking (f, h) to (r, 0), robust to tiny pairs:
+// a pair below 2^-50 is scaled by 2^100 (exact) so that f^2 + h^2 is never
+// subnormal; r is scaled back.  Branch-free: (0, 0) gives (1, 0, 0).
+// 1/sqrt(f^2 + h^2) is the hardware estimate refined by one Newton step.
 __device__ __forceinline__ float rot(float f, float h, float& c, float& s) {
-    float up = 1.0f;
     const float mx = fmaxf(fabsf(f), fabsf(h));
-    if (mx < 0x1p-50f && mx > 0.0f) {
-        int eb = 0;
-        (void)frexpf(mx, &eb);
-        f = ldexpf(f, -eb);
-        h = ldexpf(h, -eb);
-        up = ldexpf(1.0f, eb);
-    }
+    const bool tiny = mx < 0x1p-50f;
+    const float up = tiny ? 0x1p+100f : 1.0f;
+    f *= up;
+    h *= up;
     const float sq = fmaf(f, f, h * h);
-    if (sq == 0.0f) {
-        c = 1.0f;
-        s = 0.0f;
-        return 0.0f;
-    }
-    const float y = rsqrtf(sq);
-    const float ri = y * fmaf(-0.5f * sq * y, y, 1.5f);
-    c = f * ri;
+    const float y = __builtin_amdgcn_rsqf(sq);
+    float ri = y * fmaf(-0.5f * sq * y, y, 1.5f);
+    ri = sq > 0.0f ? ri : 0.0f;
+    c = sq > 0.0f ? f * ri : 1.0f;
     s = h * ri;
-    return sq * ri * up;
+    return sq * ri * (tiny ? 0x1p-100f : 1.0f);
 }
 
 template <bool VEC>
@@ -496,15 +499,26 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
 }
 
 // ---------------------------------------------------------- back-transform
-// Lane c holds column c of U_B (then V_B) in VGPRs.  Reflector k is loaded
-// by the wave (two rows per lane) one step ahead, staged in one of two LDS
-// buffers, and read back as 16-byte broadcasts; chunks above the
-// reflector's first non-zero row are skipped (wave-uniform).
+constexpr int kRB = 8;   // reflectors staged per block
+
+union BackLds {
+    struct {
+        float v[2][kRB][kMaxM];   // two blocks of reflectors
+        float tau[2][kRB];
+    };
+    float tr[kMaxN][kMaxN + 1];   // V_p, transposed on the way out
+};
+
+// Lane c holds column c of U_B (then V_B) in VGPRs.  Reflectors move in
+// blocks of kRB: the wave loads the next block (two rows per lane and
+// reflector) while it applies the current one from LDS, read back as
+// 16-byte broadcasts; chunks above a reflector's first non-zero row are
+// skipped (wave-uniform).
 __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __restrict__ ws, float* __restrict__ U,
                                                                float* __restrict__ Vt, uint32_t batch, uint32_t rows,
                                                                uint32_t cols, int trans) {
-    __shared__ __align__(16) float vb[2][kMaxM];
-    __shared__ float tr[kMaxN][kMaxN + 1];
+    __shared__ __align__(16) BackLds sb;
+    auto& tr = sb.tr;
     const int c = threadIdx.x;
     const size_t mat = blockIdx.x;
     if (mat >= batch) return;
@@ -526,45 +540,64 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
 #pragma unroll
     for (int r = kMaxN; r < kMaxM; ++r) x[r] = 0.0f;
     {
-        const int c1 = c + 64 < M ? c + 64 : M - 1;
-        float n0 = 0.0f, n1 = 0.0f, tn = 0.0f;
-        auto fetch = [&](int k) {
-            const float* v = w + W.refl() + (size_t)k * M;
-            const float p0 = v[c < M ? c : M - 1], p1 = v[c1];
-            n0 = c < M ? p0 : 0.0f;
-            n1 = c + 64 < M ? p1 : 0.0f;
-            tn = w[W.tq() + k];
+        const int c0 = c < M ? c : M - 1, c1 = c + 64 < M ? c + 64 : M - 1;
+        float n0[kRB], n1[kRB], tn = 0.0f;
+        // reflectors kb, kb - 1, .., kb - kRB + 1 (those below 0 clamped, unused)
+        auto fetch = [&](int kb) {
+#pragma unroll
+            for (int i = 0; i < kRB; ++i) {
+                const float* v = w + W.refl() + (size_t)max(kb - i, 0) * M;
+                const float p0 = v[c0], p1 = v[c1];
+                n0[i] = c < M ? p0 : 0.0f;
+                n1[i] = c + 64 < M ? p1 : 0.0f;
+            }
+            tn = c < kRB ? w[W.tq() + max(kb - c, 0)] : 0.0f;
         };
         fetch(N - 1);
-        for (int k = N - 1; k >= 0; --k) {
-            float* vk = vb[k & 1];
-            vk[c] = n0;
-            vk[c + 64] = n1;
-            const float tau = tn;
-            if (k > 0) fetch(k - 1);
-            __syncthreads();
-            if (tau == 0.0f) continue;   // uniform
-            const int j0 = k >> 2;       // v_k is zero above row k
-            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+        for (int kb = N - 1, blk = 0; kb >= 0; kb -= kRB, ++blk) {
+            float(*vk)[kMaxM] = sb.v[blk & 1];
 #pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j >= j0 && 4 * j < M) {
-                    const float4 vv = *reinterpret_cast<const float4*>(&vk[4 * j]);
-                    d0 = fmaf(vv.x, x[4 * j], d0);
-                    d1 = fmaf(vv.y, x[4 * j + 1], d1);
-                    d2 = fmaf(vv.z, x[4 * j + 2], d2);
-                    d3 = fmaf(vv.w, x[4 * j + 3], d3);
-                }
+            for (int i = 0; i < kRB; ++i) {
+                vk[i][c] = n0[i];
+                vk[i][c + 64] = n1[i];
             }
-            const float g = tau * ((d0 + d1) + (d2 + d3));
+            if (c < kRB) sb.tau[blk & 1][c] = tn;
+            if (kb - kRB >= 0) fetch(kb - kRB);
+            __syncthreads();
+#pragma unroll 1
+            for (int i = 0; i < kRB && kb - i >= 0; ++i) {
+                const int k = kb - i;
+                const float tau = sb.tau[blk & 1][i];
+                if (tau == 0.0f) continue;   // uniform
+                const float* vr = vk[i];
+                const int j0 = k >> 2;       // v_k is zero above row k
+                float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunks; ++j) {
-                if (j >= j0 && 4 * j < M) {
-                    const float4 vv = *reinterpret_cast<const float4*>(&vk[4 * j]);
-                    x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
-                    x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
-                    x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
-                    x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+                for (int g8 = 0; g8 < kChunks / 8; ++g8) {
+                    if (8 * g8 + 7 >= j0 && 32 * g8 < M) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                        for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                            const float4 vv = *reinterpret_cast<const float4*>(&vr[4 * j]);
+                            d0 = fmaf(vv.x, x[4 * j], d0);
+                            d1 = fmaf(vv.y, x[4 * j + 1], d1);
+                            d2 = fmaf(vv.z, x[4 * j + 2], d2);
+                            d3 = fmaf(vv.w, x[4 * j + 3], d3);
+                        }
+                    }
+                }
+                const float g = tau * ((d0 + d1) + (d2 + d3));
+#pragma unroll
+                for (int g8 = 0; g8 < kChunks / 8; ++g8) {
+                    if (8 * g8 + 7 >= j0 && 32 * g8 < M) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                        for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                            const float4 vv = *reinterpret_cast<const float4*>(&vr[4 * j]);
+                            x[4 * j] = fmaf(-g, vv.x, x[4 * j]);
+                            x[4 * j + 1] = fmaf(-g, vv.y, x[4 * j + 1]);
+                            x[4 * j + 2] = fmaf(-g, vv.z, x[4 * j + 2]);
+                            x[4 * j + 3] = fmaf(-g, vv.w, x[4 * j + 3]);
+                        }
+                    }
                 }
             }
         }
@@ -576,46 +609,64 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
         const float v = w[W.vb() + (size_t)(j < N ? j : N - 1) * N + cc];
         y[j] = (c < N && j < N) ? v : 0.0f;
     }
-    __syncthreads();   // the last U reflector's reads before the buffers are reused
+    __syncthreads();   // the last U block's reads before the buffers are reused
     if (N >= 2) {
-        float n0 = 0.0f, tn = 0.0f;
-        auto fetch = [&](int k) {
-            n0 = c < N ? w[W.refr() + (size_t)k * N + cc] : 0.0f;
-            tn = w[W.tp() + k];
+        float n0[kRB], tn = 0.0f;
+        auto fetch = [&](int kb) {
+#pragma unroll
+            for (int i = 0; i < kRB; ++i) {
+                const float p0 = w[W.refr() + (size_t)max(kb - i, 0) * N + cc];
+                n0[i] = c < N ? p0 : 0.0f;
+            }
+            tn = c < kRB ? w[W.tp() + max(kb - c, 0)] : 0.0f;
         };
         fetch(N - 2);
-        for (int k = N - 2; k >= 0; --k) {
-            float* uk = vb[k & 1];
-            uk[c] = n0;
-            const float tau = tn;
-            if (k > 0) fetch(k - 1);
+        for (int kb = N - 2, blk = 0; kb >= 0; kb -= kRB, ++blk) {
+            float(*uk)[kMaxM] = sb.v[blk & 1];
+#pragma unroll
+            for (int i = 0; i < kRB; ++i) uk[i][c] = n0[i];
+            if (c < kRB) sb.tau[blk & 1][c] = tn;
+            if (kb - kRB >= 0) fetch(kb - kRB);
             __syncthreads();
-            if (tau == 0.0f) continue;
-            const int j0 = (k + 1) >> 2;   // u_k is zero above entry k + 1
-            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+#pragma unroll 1
+            for (int i = 0; i < kRB && kb - i >= 0; ++i) {
+                const int k = kb - i;
+                const float tau = sb.tau[blk & 1][i];
+                if (tau == 0.0f) continue;
+                const float* ur = uk[i];
+                const int j0 = (k + 1) >> 2;   // u_k is zero above entry k + 1
+                float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kMaxN / 4; ++j) {
-                if (j >= j0 && 4 * j < N) {
-                    const float4 uu = *reinterpret_cast<const float4*>(&uk[4 * j]);
-                    d0 = fmaf(uu.x, y[4 * j], d0);
-                    d1 = fmaf(uu.y, y[4 * j + 1], d1);
-                    d2 = fmaf(uu.z, y[4 * j + 2], d2);
-                    d3 = fmaf(uu.w, y[4 * j + 3], d3);
+                for (int g8 = 0; g8 < kMaxN / 32; ++g8) {
+                    if (8 * g8 + 7 >= j0 && 32 * g8 < N) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                        for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                            const float4 uu = *reinterpret_cast<const float4*>(&ur[4 * j]);
+                            d0 = fmaf(uu.x, y[4 * j], d0);
+                            d1 = fmaf(uu.y, y[4 * j + 1], d1);
+                            d2 = fmaf(uu.z, y[4 * j + 2], d2);
+                            d3 = fmaf(uu.w, y[4 * j + 3], d3);
+                        }
+                    }
                 }
-            }
-            const float g = tau * ((d0 + d1) + (d2 + d3));
+                const float g = tau * ((d0 + d1) + (d2 + d3));
 #pragma unroll
-            for (int j = 0; j < kMaxN / 4; ++j) {
-                if (j >= j0 && 4 * j < N) {
-                    const float4 uu = *reinterpret_cast<const float4*>(&uk[4 * j]);
-                    y[4 * j] = fmaf(-g, uu.x, y[4 * j]);
-                    y[4 * j + 1] = fmaf(-g, uu.y, y[4 * j + 1]);
-                    y[4 * j + 2] = fmaf(-g, uu.z, y[4 * j + 2]);
-                    y[4 * j + 3] = fmaf(-g, uu.w, y[4 * j + 3]);
+                for (int g8 = 0; g8 < kMaxN / 32; ++g8) {
+                    if (8 * g8 + 7 >= j0 && 32 * g8 < N) {   // 8 chunks at a time: one LDS wait per group
+#pragma unroll
+                        for (int j = 8 * g8; j < 8 * g8 + 8; ++j) {
+                            const float4 uu = *reinterpret_cast<const float4*>(&ur[4 * j]);
+                            y[4 * j] = fmaf(-g, uu.x, y[4 * j]);
+                            y[4 * j + 1] = fmaf(-g, uu.y, y[4 * j + 1]);
+                            y[4 * j + 2] = fmaf(-g, uu.z, y[4 * j + 2]);
+                            y[4 * j + 3] = fmaf(-g, uu.w, y[4 * j + 3]);
+                        }
+                    }
                 }
             }
         }
     }
+    __syncthreads();   // the last V block's reads before the transpose buffer
     // outputs: tall: U = U_p (M x N), Vt = V_p^T (N x N).
     //          wide: U = V_p (rows x rows), Vt = U_p^T (rows x cols).
     if (!trans) {
