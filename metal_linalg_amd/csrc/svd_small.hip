@@ -17,19 +17,19 @@
 // A wide matrix (m < n) is solved as its transpose, the roles of U and Vt
 // swapped.  Below, "the problem" is the tall M x N (M >= N) one.
 //
-//   svd_bidiag     the problem in LDS (M x 65 floats); a wave works it,
-//                  lanes over columns for the left reflectors' products and
-//                  over rows for the right ones, so every product is a
-//                  lane-local loop over LDS (no cross-lane reductions beyond
-//                  two norms per step).  Writes d, e, the reflectors
-//                  (column-contiguous) and their tau.
+//   svd_bidiag     lane c holds column c of the problem in VGPRs (rows and
+//                  columns beyond the shape zero); left reflectors are
+//                  applied lane-locally from LDS broadcasts, right ones
+//                  through a transposed reduction in LDS.  Writes d, e, the
+//                  reflectors (column-contiguous) and their tau.
 //   svd_bdsqr      lane r holds row r of the bidiagonal's U and V in VGPRs;
 //                  the Golub-Reinsch recurrence runs on every lane with d
-//                  and e in registers (unrolled sweep, wave-uniform guards),
-//                  mirrored in LDS for the lane-parallel split test; then
-//                  sign fix, descending sort.
+//                  and e in LDS (unrolled sweep, wave-uniform guards), the
+//                  lane-parallel split test on the same arrays; then sign
+//                  fix, descending sort.
 //   svd_backtransform  lane c forms column c of U = Q [U_B; 0] and of
-//                  V = P V_B from the reflectors (wave-uniform loads).
+//                  V = P V_B from the reflectors, staged through LDS in
+//                  blocks of eight.
 #include "device_common.hpp"
 #include "kernels.hpp"
 #include "runtime.hpp"
