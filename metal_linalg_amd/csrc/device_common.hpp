@@ -100,6 +100,12 @@ __device__ __forceinline__ float hash_uniform(unsigned a, unsigned b) {
     return (float)(x >> 8) * (2.0f / 16777216.0f) - 1.0f;
 }
 
+// 1/x: the hardware estimate (about 1 ulp) refined by one Newton step.
+__device__ __forceinline__ float rcp_refined(float x) {
+    const float y = __builtin_amdgcn_rcpf(x);
+    return fmaf(y, fmaf(-x, y, 1.0f), y);
+}
+
 // A wave-level fence for LDS traffic between lanes of one wavefront: the
 // kernels that use it launch one wave per workgroup.
 __device__ __forceinline__ void wave_lds_sync() { __syncthreads(); }

@@ -43,13 +43,13 @@ constexpr float kSafeMin = 1.17549435e-38f;   // FLT_MIN
 constexpr float kPad = 0x1p100f;             // the diagonal of padding rows: never counted
 constexpr float kOrtol = 1e-3f;               // close eigenvalues: gap <= kOrtol |T| (sstein's ORTOL)
 constexpr int kMaxBisect = 64;
+constexpr int kBT = 8;                       // reflectors staged per back-transform block
 
 template <int N>
 struct alignas(16) EighLds {
-    union {
-        float stage[N][N + 1];   // the read triangle, mirrored through here
-        float vs[N][N + 4];      // the reflectors: v_k is row k (v_k[k+1] = 1)
-    };
+    // the arrays read every step first: their offsets then fit the LDS
+    // instructions' immediate fields (no address register per read)
+    float vr[2][N + 4];          // the current reflector (v_k[k+1] = 1), alternate steps
     float bc[2][N + 4];          // w of the rank-2 update, alternate steps
     float d[N + 4];       // the tridiagonal, rows >= n padded with kPad
     float e[N + 4];       // e[k] couples rows k and k+1; zero at splits and from row n - 1 on
@@ -58,6 +58,7 @@ struct alignas(16) EighLds {
     float tau[N];
     int perm[N];
     int cnt[N];
+    float bt[2][kBT][N + 4];     // back-transform: two blocks of reflectors
 };
 
 // sum of x[r] * y[r] over r in [LO, N), four partial sums
@@ -90,7 +91,7 @@ __device__ __forceinline__ float group_bcast(float v, int src) {
 // back-transformation), and read back as a broadcast for the products.
 // Then the symmetric rank-2 update of the trailing block, w through bc.
 template <int K, int N>
-__device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c, int n) {
+__device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c, int n, float* vg) {
     if constexpr (K + 2 < N) {
         if (K + 2 < n) {
             // c laundered: otherwise the compiler precomputes the lane masks
@@ -101,14 +102,15 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
             const float alpha = group_bcast<N>(xk, K + 1);
             const float ss = group_sum_dpp<N>(cl > K + 1 && cl < n ? xk * xk : 0.0f);
             float beta = alpha, tau = 0.0f, scale = 1.0f;
-            if (ss >= kTinySumsq) {
-                beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-                tau = (beta - alpha) / beta;
-                scale = 1.0f / (alpha - beta);
+            if (ss >= kTinySumsq) {   // hardware square root, refined reciprocals
+                beta = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alpha, alpha, ss)), alpha);
+                tau = (beta - alpha) * rcp_refined(beta);
+                scale = rcp_refined(alpha - beta);
             }
             const bool act = cl > K && cl < n;
             const float vc = cl == K + 1 ? 1.0f : (act ? xk * scale : 0.0f);
-            s.vs[K][c] = vc;
+            s.vr[K & 1][c] = vc;
+            if (vg && c < n) vg[(size_t)K * n + c] = vc;   // row K of V's storage, for the back-transform
             if (cl == K) {
                 s.d[K] = xk;
                 s.e[K] = beta;
@@ -117,19 +119,24 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
             wave_lds_sync();
             float v[N];
 #pragma unroll
-            for (int r = K + 1; r < N; ++r) v[r] = s.vs[K][r];
+            for (int r = K + 1; r < N; ++r) v[r] = s.vr[K & 1][r];
             const float p = act ? tau * dot_tail<K + 1, N>(v, x) : 0.0f;
             const float half = 0.5f * tau * group_sum_dpp<N>(p * vc);
             const float w = fmaf(-half, vc, p);
             float* bc = s.bc[K & 1];
             bc[c] = w;
             wave_lds_sync();
-            if (act) {
+            {
+                // every lane: outside the trailing block vc = w = 0, so the
+                // update leaves x as it is (no divergent branch, whose merge
+                // would copy the column).  v is read again from LDS: holding
+                // it across the barrier would keep N more VGPRs live.
+                const float* vr = s.vr[K & 1];
 #pragma unroll
-                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-v[r], w, fmaf(-bc[r], vc, x[r]));
+                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-vr[r], w, fmaf(-bc[r], vc, x[r]));
             }
         }
-        tridiag_step<K + 1, N>(x, s, c, n);
+        tridiag_step<K + 1, N>(x, s, c, n, vg);
     }
 }
 
@@ -176,20 +183,45 @@ __device__ __forceinline__ void normalize(float (&x)[N]) {
 }
 
 // x <- H_K x for K = K0, K0-1, ..., 0: the eigenvector of T in lane c
-// becomes that of A (Q = H_0 H_1 ... H_{n-3}).
+// becomes that of A (Q = H_0 H_1 ... H_{n-3}).  The reflectors come back
+// from V's storage (row K holds v_K) in blocks of kBT: a block is loaded
+// (element c of each reflector by lane c) one block ahead, stored to LDS and
+// read as broadcasts.  Rows past n - 3 are clamped into the matrix and
+// never used.
+template <int N>
+__device__ __forceinline__ void bt_fetch(float (&nx)[kBT], const float* vg, int kb, int c, int n) {
+    const int kmax = n - 3 > 0 ? n - 3 : 0;
+    const int cc = c < n ? c : n - 1;
+#pragma unroll
+    for (int i = 0; i < kBT; ++i) {
+        const int k = kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
+        const float v = vg[(size_t)k * n + cc];
+        nx[i] = c < n ? v : 0.0f;   // entries past n are zero
+    }
+}
+
 template <int K, int N>
-__device__ __forceinline__ void backtransform_step(float (&x)[N], const EighLds<N>& s, int n) {
+__device__ __forceinline__ void backtransform_step(float (&x)[N], EighLds<N>& s, int c, int n, const float* vg,
+                                                   float (&nx)[kBT]) {
     if constexpr (K >= 0) {
+        constexpr int B = ((N - 3) - K) / kBT;   // block of K
+        constexpr int I = ((N - 3) - K) % kBT;   // position in the block
+        if constexpr (I == 0) {
+#pragma unroll
+            for (int i = 0; i < kBT; ++i) s.bt[B & 1][i][c] = nx[i];
+            if constexpr (K - kBT >= 0) bt_fetch<N>(nx, vg, K - kBT, c, n);
+            wave_lds_sync();
+        }
         if (K + 2 < n) {
             const float tau = s.tau[K];
             float v[N];
 #pragma unroll
-            for (int r = K + 1; r < N; ++r) v[r] = s.vs[K][r];
+            for (int r = K + 1; r < N; ++r) v[r] = s.bt[B & 1][I][r];
             const float d = tau * dot_tail<K + 1, N>(v, x);
 #pragma unroll
             for (int r = K + 1; r < N; ++r) x[r] = fmaf(-d, v[r], x[r]);
         }
-        backtransform_step<K - 1, N>(x, s, n);
+        backtransform_step<K - 1, N>(x, s, c, n, vg, nx);
     }
 }
 
@@ -208,40 +240,42 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     const int nn = (int)n;
     const size_t per = (size_t)n * n;
 
-    // 1. the read triangle, mirrored into a full symmetric matrix
-    // Every row is loaded unconditionally (clamped into the matrix) so that
-    // the N loads are all in flight together; the unread triangle's values
-    // are discarded by the selects.
+    // 1. the read triangle, mirrored into a full symmetric matrix: lane c
+    // loads column c (coalesced) and row c, and takes each entry from the
+    // read triangle.  Every load is unconditional (clamped into the matrix)
+    // so that they are all in flight together.
     float x[N];
     float amax = 0.0f;
     int bad = 0;
-    const float* src = A + (live ? mat : 0) * per + (c < nn ? c : nn - 1);
+    {
+        const int cc = c < nn ? c : nn - 1;
+        const float* src = A + (live ? mat : 0) * per;
+        float xr[N];
 #pragma unroll
-    for (int r = 0; r < N; ++r) x[r] = src[(size_t)(r < nn ? r : nn - 1) * n];
+        for (int r = 0; r < N; ++r) {
+            const int rr = r < nn ? r : nn - 1;
+            x[r] = src[(size_t)rr * n + cc];
+            xr[r] = src[(size_t)cc * n + rr];
+        }
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        const bool take = live && r < nn && c < nn && (lower ? r >= c : r <= c);
-        const float v = take ? x[r] : 0.0f;
-        amax = fmaxf(amax, fabsf(v));
-        bad |= take && !finite_f(v);
-        s.stage[r][c] = v;
-        x[r] = v;
-    }
-    wave_lds_sync();
-#pragma unroll
-    for (int r = 0; r < N; ++r) {
-        const bool take = lower ? r >= c : r <= c;
-        if (live && r < nn && c < nn && !take) x[r] = s.stage[c][r];
+        for (int r = 0; r < N; ++r) {
+            const bool in = live && r < nn && c < nn;
+            const bool take = lower ? r >= c : r <= c;
+            const float v = in ? (take ? x[r] : xr[r]) : 0.0f;
+            amax = fmaxf(amax, fabsf(v));
+            bad |= in && take && !finite_f(v);
+            x[r] = v;
+        }
     }
     amax = group_max<N>(amax);
     bad = group_or<N>(bad);
     const int ex = bad ? 0 : scale_exponent(amax);
 #pragma unroll
     for (int r = 0; r < N; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -ex);
-    wave_lds_sync();
 
-    // 2. tridiagonalise: d, e, tau, and v_k in lane k's column
-    tridiag_step<0, N>(x, s, c, nn);
+    // 2. tridiagonalise: d, e, tau; v_k goes to row k of V's storage
+    float* vg = (VEC && live) ? V + mat * per : nullptr;
+    tridiag_step<0, N>(x, s, c, nn, vg);
     {
         float diag = 0.0f, sub = 0.0f;
 #pragma unroll
@@ -389,11 +423,19 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
         for (int pass = 0; pass < (all_diag ? 0 : 2); ++pass) {
             float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
+            // d and e of the next row are read one step ahead (their LDS
+            // latency hides behind this step's recurrence)
+            float enow = s.e[0], dnx = s.d[1], enx = s.e[1];
 #pragma unroll
             for (int k = 0; k < N; ++k) {
                 if (k + 1 < N) {
-                    const float ek = s.e[k];
-                    const float an = s.d[k + 1] - lam, cn = s.e[k + 1], b1 = x[k + 1];
+                    const float ek = enow;
+                    const float an = dnx - lam, cn = enx, b1 = x[k + 1];
+                    enow = enx;
+                    if (k + 2 < N) {
+                        dnx = s.d[k + 2];
+                        enx = s.e[k + 2];
+                    }
                     const bool keep = fabsf(a) >= fabsf(ek);
                     const float piv = keep ? a : ek;
                     const float r0 = __builtin_amdgcn_rcpf(fabsf(piv) < tol ? copysignf(tol, piv) : piv);
@@ -416,11 +458,17 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
             // loop's copies live across it
             __asm__ volatile("" ::: "memory");
             float x1 = 0.0f, x2 = 0.0f;
+            float rnx = s.re[N - 2], dnx2 = s.d[N - 1], enx2 = s.e[N - 1];   // one step ahead
 #pragma unroll
             for (int k = N - 1; k >= 0; --k) {
                 float xv = x[k];
                 if (k + 1 < N) {
-                    const float rk = s.re[k], dk1 = s.d[k + 1], ek1 = s.e[k + 1];
+                    const float rk = rnx, dk1 = dnx2, ek1 = enx2;
+                    if (k > 0) {
+                        rnx = s.re[k - 1];
+                        dnx2 = s.d[k];
+                        enx2 = s.e[k];
+                    }
                     const bool swapped = u[k] != u[k];
                     const float q1 = swapped ? (dk1 - lam) * rk : u[k];
                     const float q2 = swapped ? ek1 * rk : 0.0f;
@@ -457,8 +505,15 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
             for (int k = 0; k < N; ++k) x[k] = k == row ? 1.0f : 0.0f;
         }
 
-        // 7. back to A's basis; lane c writes column c of V
-        backtransform_step<N - 3, N>(x, s, nn);
+        // 7. back to A's basis; lane c writes column c of V (over the
+        // reflectors: every lane's loads of them have returned by the last
+        // barrier of the back-transform)
+        {
+            float nx[kBT];
+            const float* vsrc = V + (live ? mat : 0) * per;
+            bt_fetch<N>(nx, vsrc, N - 3, c, nn);
+            backtransform_step<N - 3, N>(x, s, c, nn, vsrc, nx);
+        }
         if (live && mine) {
             float* dst = V + mat * per;
 #pragma unroll
