@@ -24,8 +24,11 @@
 // LDS as float4 broadcasts), then solves for its own eigenvector with the
 // pivoted factor, right-hand side and back substitution in VGPRs.  Lanes of
 // a close group exchange vectors with cross-lane permutes, one member per
-// round.  Lane c then applies the reflectors to its vector and writes column
-// c of V; lanes write consecutive addresses.  The previous design ran
+// round.  The reflectors wait in V's own storage (row k holds v_k) and come
+// back through LDS eight at a time; lane c applies them to its vector and
+// writes column c of V over them; lanes write consecutive addresses.  LDS
+// holds only the current reflector, w, the tridiagonal and a staging block
+// (7.3 KB at n = 64), so three waves fit per SIMD.  The previous design ran
 // implicit QL on every lane redundantly: a serial rotation chain that kept
 // 63 of 64 lanes idle (the bisection and the solves need ~30x fewer issue
 // slots per matrix).
