@@ -156,39 +156,44 @@ __device__ __forceinline__ float dot_from(const float* x, const float* y) {
 }
 
 // Factorization step J of the fixed-shape kernel (compile-time J, so every
-// row predicate folds away and only rows >= J are touched).
+// row predicate folds away and only rows >= J are touched).  Lane J
+// publishes its column unscaled with the reflector's tau and scale (the
+// other lanes fold the scale into their products), and every lane scales its
+// own reflector once after the last step: one multiply per row instead of a
+// one-lane pass per step.  Square root and reciprocals are the hardware's,
+// the reciprocals refined by one Newton step.
 template <int J, int M, int N, int G, int LD>
-__device__ __forceinline__ void qr_fixed_step(float (&x)[M], float (&vsh)[LD], float* tsh, int c) {
+__device__ __forceinline__ void qr_fixed_step(float (&x)[M], float (&vsh)[LD], float* tsh, float* ssh, int c) {
     if constexpr (J < (M < N ? M : N)) {
         float ss = dot_from<J + 1, M>(x, x);
         const float alpha = x[J];
         float beta = alpha, tau = 0.0f, scale = 1.0f;
         if (ss >= kTinySumsq) {
-            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-            tau = (beta - alpha) / beta;
-            scale = 1.0f / (alpha - beta);
+            beta = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alpha, alpha, ss)), alpha);
+            tau = (beta - alpha) * rcp_refined(beta);
+            scale = rcp_refined(alpha - beta);
         }
         if (c == J) {
             x[J] = beta;
 #pragma unroll
-            for (int r = J + 1; r < M; ++r) {
-                x[r] *= scale;
-                vsh[r] = x[r];
-            }
-            vsh[J] = 1.0f;
+            for (int r = J + 1; r < M; ++r) vsh[r] = x[r];
             tsh[J] = tau;
+            ssh[J] = scale;
         }
         wave_lds_sync();
         if (c > J) {
             float v[M];
 #pragma unroll
-            for (int r = J; r < M; ++r) v[r] = vsh[r];
-            const float d = tsh[J] * dot_from<J, M>(v, x);
+            for (int r = J + 1; r < M; ++r) v[r] = vsh[r];
+            const float sc = ssh[J];
+            const float d = tsh[J] * fmaf(sc, dot_from<J + 1, M>(v, x), x[J]);
+            const float ds = d * sc;
+            x[J] -= d;
 #pragma unroll
-            for (int r = J; r < M; ++r) x[r] = fmaf(-d, v[r], x[r]);
+            for (int r = J + 1; r < M; ++r) x[r] = fmaf(-ds, v[r], x[r]);
         }
         wave_lds_sync();
-        qr_fixed_step<J + 1, M, N, G, LD>(x, vsh, tsh, c);
+        qr_fixed_step<J + 1, M, N, G, LD>(x, vsh, tsh, ssh, c);
     }
 }
 
@@ -229,6 +234,7 @@ __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ 
     constexpr int LD = M + 4;   // per-group stride, off the other group's banks
     __shared__ float vsh[MPW][LD];
     __shared__ float tsh[MPW][N];
+    __shared__ float ssh[MPW][N];   // the reflectors' scales
     const int lane = threadIdx.x;
     const int c = lane % G;
     const int g = lane / G;
@@ -253,7 +259,12 @@ __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ 
 #pragma unroll
     for (int r = 0; r < M; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
 
-    qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], c);
+    qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], ssh[g], c);
+    {   // lane c's reflector below the diagonal, scaled now
+        const float sc = ssh[g][c < N ? c : 0];
+#pragma unroll
+        for (int r = 0; r < M; ++r) x[r] = r > c ? x[r] * sc : x[r];
+    }
 
     if (live && c < N) {
         float* out_r = Rout + mat * N * N;
