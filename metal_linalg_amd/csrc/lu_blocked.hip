@@ -631,21 +631,23 @@ void launch_leaf(float* A, int n, int pc, int pj, int pe, int w, uint32_t* piv, 
     hipLaunchKernelGGL((lu_leaf_kernel<RPT, W>), dim3(1), dim3(LT), 0, s, A, n, pc, pj, pe, w, piv, info);
 }
 
-// the leaf shape for an n x n factorization: rows per thread and width
+// the leaf shape for the rows it holds (pc .. n - 1): rows per thread and
+// width; later leaves hold fewer rows and get fewer rows per thread
 void leaf(float* A, int n, int pc, int pj, int pe, uint32_t* piv, uint32_t* info, hipStream_t s, int& width) {
-    if (n <= LT) {
+    const int m = n - pc;
+    if (m <= LT) {
         width = 16;
         launch_leaf<1, 16>(A, n, pc, pj, pe, std::min(16, pe - pc), piv, info, s);
-    } else if (n <= 2 * LT) {
+    } else if (m <= 2 * LT) {
         width = 16;
         launch_leaf<2, 16>(A, n, pc, pj, pe, std::min(16, pe - pc), piv, info, s);
-    } else if (n <= 4 * LT) {
+    } else if (m <= 4 * LT) {
         width = 16;
         launch_leaf<4, 16>(A, n, pc, pj, pe, std::min(16, pe - pc), piv, info, s);
-    } else if (n <= 8 * LT) {
+    } else if (m <= 8 * LT) {
         width = 16;
         launch_leaf<8, 16>(A, n, pc, pj, pe, std::min(16, pe - pc), piv, info, s);
-    } else if (n <= 16 * LT) {
+    } else if (m <= 16 * LT) {
         width = 8;
         launch_leaf<16, 8>(A, n, pc, pj, pe, std::min(8, pe - pc), piv, info, s);
     } else {
