@@ -24,7 +24,7 @@
 // LDS as float4 broadcasts), then solves for its own eigenvector with the
 // pivoted factor, right-hand side and back substitution in VGPRs.  Lanes of
 // a close group exchange vectors with cross-lane permutes, one member per
-// round.  The reflectors wait in V's own storage (row k holds v_k) and come
+// round.  The reflectors wait in V's own storage (packed lower parts) and come
 // back through LDS eight at a time; lane c applies them to its vector and
 // writes column c of V over them; lanes write consecutive addresses.  LDS
 // holds only the current reflector, w, the tridiagonal and a staging block
@@ -78,6 +78,11 @@ __device__ __forceinline__ float dot_tail(const float* x, const float* y) {
     return (s0 + s1) + (s2 + s3);
 }
 
+// Where v_K's entries K+1 .. n-1 start in the packed reflector storage:
+// after v_0 .. v_{K-1} (n-1, n-2, ... entries).  The whole set, n(n-1)/2 - 1
+// floats, fits in V's n x n.
+__device__ __forceinline__ int refl_offset(int K, int n) { return K * (n - 1) - K * (K - 1) / 2; }
+
 // ssytd2 (lower) step K: reflector from column K below the subdiagonal, then
 // the symmetric rank-2 update of the trailing block.
 // The value of lane `src` of the group, on every lane of the group.
@@ -113,7 +118,9 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
             const bool act = cl > K && cl < n;
             const float vc = cl == K + 1 ? 1.0f : (act ? xk * scale : 0.0f);
             s.vr[K & 1][c] = vc;
-            if (vg && c < n) vg[(size_t)K * n + c] = vc;   // row K of V's storage, for the back-transform
+            // entries K+1 .. n-1 of v_K, packed after those of v_0 .. v_{K-1}
+            // in V's storage, for the back-transform
+            if (vg && cl > K && c < n) vg[refl_offset(K, n) + c - K - 1] = vc;
             if (cl == K) {
                 s.d[K] = xk;
                 s.e[K] = beta;
@@ -187,19 +194,20 @@ __device__ __forceinline__ void normalize(float (&x)[N]) {
 
 // x <- H_K x for K = K0, K0-1, ..., 0: the eigenvector of T in lane c
 // becomes that of A (Q = H_0 H_1 ... H_{n-3}).  The reflectors come back
-// from V's storage (row K holds v_K) in blocks of kBT: a block is loaded
-// (element c of each reflector by lane c) one block ahead, stored to LDS and
-// read as broadcasts.  Rows past n - 3 are clamped into the matrix and
-// never used.
+// from V's storage (packed: entries K+1 .. n-1 of v_K from
+// refl_offset(K, n)) in blocks of kBT: a block is loaded (element c of each
+// reflector by lane c) one block ahead, stored to LDS and read as
+// broadcasts.  Reflectors past n - 3 are clamped into range and never used.
 template <int N>
 __device__ __forceinline__ void bt_fetch(float (&nx)[kBT], const float* vg, int kb, int c, int n) {
     const int kmax = n - 3 > 0 ? n - 3 : 0;
-    const int cc = c < n ? c : n - 1;
 #pragma unroll
     for (int i = 0; i < kBT; ++i) {
         const int k = kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
-        const float v = vg[(size_t)k * n + cc];
-        nx[i] = c < n ? v : 0.0f;   // entries past n are zero
+        const bool in = c > k && c < n;   // v_k is zero at and above row k
+        const int off = refl_offset(k, n);
+        const float v = vg[in ? off + c - k - 1 : off];
+        nx[i] = in ? v : 0.0f;
     }
 }
 
@@ -276,7 +284,7 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
 #pragma unroll
     for (int r = 0; r < N; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -ex);
 
-    // 2. tridiagonalise: d, e, tau; v_k goes to row k of V's storage
+    // 2. tridiagonalise: d, e, tau; v_k goes to V's storage (packed)
     float* vg = (VEC && live) ? V + mat * per : nullptr;
     tridiag_step<0, N>(x, s, c, nn, vg);
     {
