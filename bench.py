@@ -39,8 +39,8 @@ FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
 # x1.9998, WRITE_SIZE x1.0); the runs and the scaling are in
 # profiles/<kernel>_<workload>.md.  Workloads not yet counted report null.
 TRAFFIC_BYTES = {
-    "eigh": 74_606_375 + 68_292_919,   # profiles/eigh_small_eigh.md
-    "qr": 42_169_219 + 81_920_000,     # profiles/qr_small_qr.md
+    "eigh": 106_810_252 + 97_147_822,  # profiles/eigh_small_eigh.md
+    "qr": 41_840_322 + 81_920_000,     # profiles/qr_small_qr.md
 }
 
 
