@@ -257,23 +257,22 @@ struct BdLds {
     int perm[kMaxN];
 };
 
-// (c, s, r) of the rotation taking (f, h) to (r, 0), robust to tiny pairs:
-// a pair below 2^-50 is scaled by 2^100 (exact) so that f^2 + h^2 is never
-// subnormal; r is scaled back.  Branch-free: (0, 0) gives (1, 0, 0).
-// 1/sqrt(f^2 + h^2) is the hardware estimate refined by one Newton step.
+// (c, s, r) of the rotation taking (f, h) to (r, 0).  A pair with
+// f^2 + h^2 below 2^-100 (entries below 2^-50, far under the convergence
+// tolerance of a matrix scaled into [0.5, 1)) gives the identity and r = 0:
+// an orthogonal rotation either way, off by less than 2^-50 in what it
+// leaves behind, and never a rotation built from a subnormal sum of squares.
+// Branch-free; 1/sqrt(f^2 + h^2) is the hardware estimate refined by one
+// Newton step.
 __device__ __forceinline__ float rot(float f, float h, float& c, float& s) {
-    const float mx = fmaxf(fabsf(f), fabsf(h));
-    const bool tiny = mx < 0x1p-50f;
-    const float up = tiny ? 0x1p+100f : 1.0f;
-    f *= up;
-    h *= up;
     const float sq = fmaf(f, f, h * h);
+    const bool ok = sq >= 0x1p-100f;
     const float y = __builtin_amdgcn_rsqf(sq);
     float ri = y * fmaf(-0.5f * sq * y, y, 1.5f);
-    ri = sq > 0.0f ? ri : 0.0f;
-    c = sq > 0.0f ? f * ri : 1.0f;
+    ri = ok ? ri : 0.0f;
+    c = ok ? f * ri : 1.0f;
     s = h * ri;
-    return sq * ri * (tiny ? 0x1p-100f : 1.0f);
+    return sq * ri;
 }
 
 template <bool VEC>
