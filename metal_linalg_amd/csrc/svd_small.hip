@@ -128,9 +128,10 @@ __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict_
         const float ss = wave_sum_f(fmaf(l0, l0, a1 * a1));
         float beta = alpha, tau = 0.0f, scale = 1.0f;
         if (ss >= kTinySumsq) {
-            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-            tau = (beta - alpha) / beta;
-            scale = 1.0f / (alpha - beta);
+            // hardware square root, refined reciprocals (about 1 ulp)
+            beta = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alpha, alpha, ss)), alpha);
+            tau = (beta - alpha) * rcp_refined(beta);
+            scale = rcp_refined(alpha - beta);
         }
         __syncthreads();   // every read of column k before the reflector replaces it
         const float v0 = c < k ? 0.0f : (c == k ? 1.0f : a0 * scale);
@@ -191,9 +192,9 @@ __global__ __launch_bounds__(64) void svd_bidiag_kernel(const float* __restrict_
         const float ssr = wave_sum_f(ur * ur);
         float br = alr, taur = 0.0f, scr = 1.0f;
         if (ssr >= kTinySumsq) {
-            br = -copysignf(sqrtf(fmaf(alr, alr, ssr)), alr);
-            taur = (br - alr) / br;
-            scr = 1.0f / (alr - br);
+            br = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alr, alr, ssr)), alr);
+            taur = (br - alr) * rcp_refined(br);
+            scr = rcp_refined(alr - br);
         }
         const float up = c == k + 1 ? 1.0f : ur * scr;   // u_c, 0 for c <= k
         if (vectors && c < N) w[W.refr() + (size_t)k * N + c] = up;
