@@ -148,24 +148,33 @@ __global__ __launch_bounds__(256) void sytrd_col_kernel(SytrdArgs g) {
     }
     float tp = 0.0f, alpha2 = 0.0f;
     if (ip >= 0) {
-        // the previous column's partial dots: qV[k], qW[k] (k < ip), y^T v
+        // the previous column's partial dots: qV[k], qW[k] (k < ip), y^T v.
+        // Two threads per slot (nv <= 2 NBT - 1 <= 127 slots: one pass of
+        // 256 threads), each summing half of the workgroups' partials, so
+        // that one round of loads (32 float4 each at n <= 4096) covers it
         const int nv = 2 * ip + 1;
-        for (int x = t; x < nv; x += 256) {
-            const int slot = x < ip ? x : (x < 2 * ip ? NBT + (x - ip) : 2 * NBT);
+        const int hn = ((g.nwgB + 7) >> 3) << 2;   // half of nwgB, rounded up to a multiple of 4
+        const bool vec4 = (g.nwgB & 3) == 0;
+        for (int x0 = 0; x0 < nv; x0 += 128) {
+            const int x = x0 + (t >> 1), hf = t & 1;
+            const bool live = x < nv;
+            const int xs = live ? x : 0;
+            const int slot = xs < ip ? xs : (xs < 2 * ip ? NBT + (xs - ip) : 2 * NBT);
             const float* ps = g.partB + (size_t)slot * g.nwgB;
+            const int bb = hf * hn, be = min(g.nwgB, bb + hn);
             float acc = 0.0f;
-            if ((g.nwgB & 3) == 0) {
-                for (int b0 = 0; b0 < g.nwgB; b0 += 128) {
+            if (vec4) {
+                for (int b0 = bb; b0 < be; b0 += 128) {
                     float4 pv[32];
 #pragma unroll
                     for (int u = 0; u < 32; ++u) {
                         const int b = b0 + 4 * u;
-                        pv[u] = *reinterpret_cast<const float4*>(ps + (b < g.nwgB ? b : 0));
+                        pv[u] = *reinterpret_cast<const float4*>(ps + (b < be ? b : 0));
                     }
                     float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int u = 0; u < 32; ++u)
-                        if (b0 + 4 * u < g.nwgB) {
+                        if (b0 + 4 * u < be) {
                             s4[0] += pv[u].x;
                             s4[1] += pv[u].y;
                             s4[2] += pv[u].z;
@@ -174,15 +183,16 @@ __global__ __launch_bounds__(256) void sytrd_col_kernel(SytrdArgs g) {
                     acc += (s4[0] + s4[1]) + (s4[2] + s4[3]);
                 }
             } else {
-                for (int b = 0; b < g.nwgB; ++b) acc += ps[b];
+                for (int b = bb; b < be; ++b) acc += ps[b];
             }
-            q[x] = acc;
+            acc += __shfl_xor(acc, 1, 64);
+            if (live && hf == 0) q[x] = acc;
         }
         __syncthreads();
         tp = g.tau[g.j0 + ip];
-        // w^T v before the correction = tau (y^T v - 2 qV . qW)
-        float qq = 0.0f;
-        for (int k = 0; k < ip; ++k) qq = fmaf(q[k], q[ip + k], qq);
+        // w^T v before the correction = tau (y^T v - 2 qV . qW); ip < 64,
+        // so one lane per k and a wave sum
+        const float qq = wave_sum_f(lane < ip ? q[lane] * q[ip + (lane < ip ? lane : 0)] : 0.0f);
         alpha2 = -0.5f * tp * (tp * (q[2 * ip] - 2.0f * qq));
     }
     // W[row, ip] = tau (y - W qV - V qW) + alpha' v  (rows >= j)
@@ -200,14 +210,14 @@ __global__ __launch_bounds__(256) void sytrd_col_kernel(SytrdArgs g) {
     }
     if (!g.update) return;
     __syncthreads();   // rowj
-    if (t == 0) {
+    if (t < 64) {   // wave 0: one lane per k
         float wv0 = 0.0f;
         if (ip >= 0) {
-            float sp = 0.0f;
-            for (int k = 0; k < ip; ++k) sp = fmaf(rowj[NBT + k], q[k], fmaf(rowj[k], q[ip + k], sp));
+            const int k = lane < ip ? lane : 0;
+            const float sp = wave_sum_f(lane < ip ? fmaf(rowj[NBT + k], q[k], rowj[k] * q[ip + k]) : 0.0f);
             wv0 = fmaf(tp, g.y[j] - sp, alpha2 * rowj[ip]);
         }
-        wj = wv0;
+        if (t == 0) wj = wv0;
     }
     __syncthreads();
     // a = A[:, j] - V W[j, :]^T - W V[j, :]^T on rows >= j
