@@ -118,8 +118,10 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
     float* dv = v ? call.out(v, (size_t)B * n * n) : nullptr;
     uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
     if (small) {
+        // no convergence read-back: bisection always ends (every info word
+        // carries bit 16, or bit 17 for a non-finite matrix), so the
+        // reference's non-convergence error cannot arise on this path
         eigh_small(da, dw, dv, di, B, n, lower, call.stream());
-        check_converged(di, B, call.stream(), "eigh");
     } else {
         const size_t floats = eigh_sytrd_floats(n) + eigh_tridiag_floats(n);
         float* work = static_cast<float*>(call.scratch(floats * sizeof(float)));
