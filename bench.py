@@ -8,7 +8,11 @@ pointers).  W untimed steps, then K timed steps between two
 synchronisations.  One JSON line on stdout: `value` = matrices/s over the
 timed steps; `roofline` = the dominant kernel's algorithmic bytes (or flops)
 per launch over its average duration, timed with HIP events on the
-library's launch stream during the timed steps; `cpu_baseline` = the oracle
+library's launch stream during the timed steps (for the batched kernels,
+which issue-bound VALU work rather than HBM bytes limits, `roofline.valu_issue`
+adds their measured VALU instruction count per call as issue time on 1024
+SIMDs at 2.4 GHz, and its fraction of the measured kernel time);
+`cpu_baseline` = the oracle
 (the reference's LAPACK-batched CPU path restated) on the host's cores over
 a bounded sample of the same workload.
 
@@ -42,6 +46,17 @@ TRAFFIC_BYTES = {
     "eigh": 106_810_252 + 97_147_822,  # profiles/eigh_small_eigh.md
     "qr": 41_840_322 + 81_920_000,     # profiles/qr_small_qr.md
 }
+
+# The batched kernels are bound by instruction issue, not HBM: VALU
+# instructions per call (rocprofv3 --pmc SQ_INSTS_VALU, summed over the
+# call's kernels; profiles/valu_instructions.md).  A wave64 VALU instruction
+# occupies its SIMD for 4 cycles; MI355X has 1024 SIMDs at 2.4 GHz.
+VALU_INSTRUCTIONS = {
+    "qr": 36_865_000,
+    "eigh": 139_619_150,
+    "svd": 93_806_592 + 179_735_668 + 51_152_896,
+}
+SIMDS, CLOCK_HZ = 1024, 2.4e9
 
 
 class Workload:
@@ -281,6 +296,11 @@ def main():
     roof["kernel_us_per_call"] = round(kernel_s_per_call * 1e6, 3)
     roof["algorithmic_bytes_per_launch"] = wl.bytes_per_call
     roof["algorithmic_flops_per_launch"] = wl.flops_per_call
+    if wl.name in VALU_INSTRUCTIONS:
+        issue_s = VALU_INSTRUCTIONS[wl.name] * 4 / (SIMDS * CLOCK_HZ)
+        roof["valu_issue"] = {"instructions_per_call": VALU_INSTRUCTIONS[wl.name],
+                              "issue_us_per_call": round(issue_s * 1e6, 1),
+                              "frac": round(issue_s / kernel_s_per_call, 4)}
 
     # host-pointer (PCIe-inclusive) rate, for the record; never `value`
     t0 = time.perf_counter()
