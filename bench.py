@@ -8,10 +8,11 @@ pointers).  W untimed steps, then K timed steps between two
 synchronisations.  One JSON line on stdout: `value` = matrices/s over the
 timed steps; `roofline` = the dominant kernel's algorithmic bytes (or flops)
 per launch over its average duration, timed with HIP events on the
-library's launch stream during the timed steps (for the batched kernels,
-which issue-bound VALU work rather than HBM bytes limits, `roofline.valu_issue`
-adds their measured VALU instruction count per call as issue time on 1024
-SIMDs at 2.4 GHz, and its fraction of the measured kernel time);
+library's launch stream during the timed steps (the batched kernels are
+limited by VALU instruction issue rather than HBM bytes, so
+`roofline.valu_issue` adds their measured VALU instruction count per call as
+issue time on 1024 SIMDs at 2.4 GHz, and its fraction of the measured kernel
+time);
 `cpu_baseline` = the oracle
 (the reference's LAPACK-batched CPU path restated) on the host's cores over
 a bounded sample of the same workload.
