@@ -129,7 +129,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const int lane = t & 63;
     const int wave = t >> 6;
     const int wm = (wave & 1) * 64, wn = (wave >> 1) * 64;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // Tile order: workgroups are dispatched round-robin over the eight XCDs,
+    // each with its own L2, so consecutive workgroup ids go to different
+    // XCDs.  Renumber so that each XCD takes a contiguous range of tiles,
+    // and walk that range in bands of 8 tile rows (a band's tiles share A's
+    // row panels and, band by band, B's column panels in that XCD's L2).
+    int ty = blockIdx.y, tx = blockIdx.x;
+    {
+        const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
+        const int bid = blockIdx.y * gx + blockIdx.x;
+        const int lin = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+        constexpr int GM = 8;
+        const int in_group = GM * gx;
+        const int first = (lin / in_group) * GM;
+        const int gm = min(gy - first, GM);
+        const int r = lin - (lin / in_group) * in_group;
+        ty = first + r % gm;
+        tx = r / gm;
+    }
+    const int m0 = ty * BM, n0 = tx * BN;
     if (g.lower && n0 >= m0 + BM) return;   // tile strictly above the diagonal (uniform)
     const size_t bz = blockIdx.z;
     const float* A = g.A + bz * g.sa;
