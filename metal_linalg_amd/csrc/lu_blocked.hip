@@ -359,14 +359,26 @@ __global__ __launch_bounds__(LT) void lu_leaf_kernel(float* __restrict__ P, int 
     if (t < ncr) {
         const int cc = ncl + t;
         float x[W];
+        if (w == W) {   // uniform; the usual case: no branch per row, so the
+                        // LDS reads of all rows can be in flight together
 #pragma unroll
-        for (int i = 0; i < W; ++i) {
-            if (i < w) {
+            for (int i = 0; i < W; ++i) {
                 float s = stage[i][cc];
 #pragma unroll
                 for (int l = 0; l < i; ++l) s = fmaf(-Ls[i][l], x[l], s);
                 x[i] = s;
                 stage[i][cc] = s;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < W; ++i) {
+                if (i < w) {
+                    float s = stage[i][cc];
+#pragma unroll
+                    for (int l = 0; l < i; ++l) s = fmaf(-Ls[i][l], x[l], s);
+                    x[i] = s;
+                    stage[i][cc] = s;
+                }
             }
         }
     }
