@@ -55,7 +55,7 @@ TRAFFIC_BYTES = {
 VALU_INSTRUCTIONS = {
     "qr": 36_865_000,
     "eigh": 139_619_150,
-    "svd": 93_806_592 + 179_735_668 + 51_152_896,
+    "svd": 93_806_592 + 162_341_627 + 51_152_896,
 }
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
