@@ -121,7 +121,9 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
         // no convergence read-back: bisection always ends (every info word
         // carries bit 16, or bit 17 for a non-finite matrix), so the
         // reference's non-convergence error cannot arise on this path
-        eigh_small(da, dw, dv, di, B, n, lower, call.stream());
+        const size_t wsb = eigh_small_workspace(n, B, dv != nullptr);
+        float* ws = wsb ? static_cast<float*>(call.scratch(wsb)) : nullptr;
+        eigh_small(da, dw, dv, di, B, n, lower, ws, call.stream());
     } else {
         const size_t floats = eigh_sytrd_floats(n) + eigh_tridiag_floats(n);
         float* work = static_cast<float*>(call.scratch(floats * sizeof(float)));

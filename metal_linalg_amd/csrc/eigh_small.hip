@@ -28,7 +28,11 @@
 // back through LDS eight at a time; lane c applies them to its vector and
 // writes column c of V over them; lanes write consecutive addresses.  LDS
 // holds only the current reflector, w, the tridiagonal and a staging block
-// (7.3 KB at n = 64), so three waves fit per SIMD.  The previous design ran
+// (7.3 KB at n = 64).  With vectors at n = 64 the work runs in two launches:
+// the tridiagonalisation and the bisection fit 128 VGPRs (four waves per
+// SIMD, so a 4096-matrix batch is resident at once), the inverse iteration
+// needs ~150 (three); the first saves the tridiagonal, the eigenvalues and
+// tau for the second (1.5 KB per matrix).  The previous design ran
 // implicit QL on every lane redundantly: a serial rotation chain that kept
 // 63 of 64 lanes idle (the bisection and the solves need ~30x fewer issue
 // slots per matrix).
@@ -47,6 +51,12 @@ constexpr float kPad = 0x1p100f;             // the diagonal of padding rows: ne
 constexpr float kOrtol = 1e-3f;               // close eigenvalues: gap <= kOrtol |T| (sstein's ORTOL)
 constexpr int kMaxBisect = 64;
 constexpr int kBT = 8;                       // reflectors staged per back-transform block
+// n = 64 with vectors runs in two launches (the first fits four waves per
+// SIMD, the vectors need more VGPRs): per matrix the first leaves d, e, 1/e,
+// tau, the eigenvalue and the diagonal-path row of each lane, and three
+// scalars for the second
+constexpr int kSplitN = 64;
+constexpr int kSplitFloats = 6 * kSplitN + 4;
 
 template <int N>
 struct alignas(16) EighLds {
@@ -127,10 +137,19 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
                 s.tau[K] = tau;
             }
             wave_lds_sync();
-            float v[N];
+            // v^T x_c, v read from LDS 16 rows at a time (the schedule
+            // barriers keep the compiler from holding all of v in VGPRs
+            // beside the column)
+            float dp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            {
+                const float* vr = s.vr[K & 1];
 #pragma unroll
-            for (int r = K + 1; r < N; ++r) v[r] = s.vr[K & 1][r];
-            const float p = act ? tau * dot_tail<K + 1, N>(v, x) : 0.0f;
+                for (int r = K + 1; r < N; ++r) {
+                    dp[r & 3] = fmaf(vr[r], x[r], dp[r & 3]);
+                    if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            const float p = act ? tau * ((dp[0] + dp[1]) + (dp[2] + dp[3])) : 0.0f;
             const float half = 0.5f * tau * group_sum_dpp<N>(p * vc);
             const float w = fmaf(-half, vc, p);
             float* bc = s.bc[K & 1];
@@ -236,10 +255,143 @@ __device__ __forceinline__ void backtransform_step(float (&x)[N], EighLds<N>& s,
     }
 }
 
-template <int N, bool VEC>
-__global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict__ A, float* __restrict__ W,
+// Stage 5-7 for lane c of group g: inverse iteration for the eigenvector
+// of lam, MGS inside close groups, back-transform by the reflectors kept in
+// V's storage, and column c of V written.  s holds d, e, 1/e and tau.
+template <int N>
+__device__ __forceinline__ void eigh_vectors(EighLds<N>& s, float (&x)[N], float* __restrict__ V, int c, int g,
+                                             size_t mat, bool live, int nn, uint32_t n, size_t per, float lam,
+                                             bool mine, bool diag, int row, bool all_diag, float tnorm, int bad) {
+    // 5. inverse iteration: T - lam I = P L U with partial pivoting
+    // (slagtf), the right-hand side carried along.  x[k] holds the
+    // right-hand side, then row k of U scaled by its pivot (x, and u =
+    // the superdiagonal entry where row k kept its place), then the
+    // solution.  Where rows k and k+1 were swapped (u = NaN), U's row is
+    // (e_k, d_{k+1} - lam, e_{k+1}), rebuilt from LDS on the way back.
+    // The whole tridiagonal is solved: at a split (e = 0) the
+    // elimination decouples, and rows past n (kPad, e = 0) carry zeros.
+    // Eigenvectors of other blocks with an eigenvalue as close as this
+    // one's fall into its close group below.
+    const float tol = fmaxf(kEps * tnorm, kSafeMin);   // smaller pivots become +-tol
+    float u[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)(mat * 64 + c), (uint32_t)k) : 0.0f;
+    // close eigenvalues: lanes cs .. c with gaps <= kOrtol |T|
+    const float prev = __shfl_up(lam, 1, N);
+    const bool brk = c == 0 || !mine || diag || lam - prev > kOrtol * tnorm;
+    uint64_t brks = __ballot(brk);
+    if (N < 64) brks = (brks >> (g * N)) & ((1ull << N) - 1);
+    const int cs = 63 - __clzll((unsigned long long)(brks & ((2ull << c) - 1)));
+    const int pos = c - cs;
+    int rounds = pos;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
+    for (int pass = 0; pass < (all_diag ? 0 : 2); ++pass) {
+        float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
+        // d and e of the next row are read one step ahead (their LDS
+        // latency hides behind this step's recurrence)
+        float enow = s.e[0], dnx = s.d[1], enx = s.e[1];
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            if (k + 1 < N) {
+                const float ek = enow;
+                const float an = dnx - lam, cn = enx, b1 = x[k + 1];
+                enow = enx;
+                if (k + 2 < N) {
+                    dnx = s.d[k + 2];
+                    enx = s.e[k + 2];
+                }
+                const bool keep = fabsf(a) >= fabsf(ek);
+                const float piv = keep ? a : ek;
+                const float r0 = __builtin_amdgcn_rcpf(fabsf(piv) < tol ? copysignf(tol, piv) : piv);
+                const float l = (keep ? ek : a) * r0;
+                x[k] = (keep ? b0 : b1) * r0;
+                u[k] = keep ? cc * r0 : qnan();   // NaN marks a swap
+                // pinned: computed here, not sunk into the backward loop
+                // with their factors kept live instead
+                __asm__ volatile("" : "+v"(x[k]), "+v"(u[k]));
+                const float na = keep ? fmaf(-l, cc, an) : fmaf(-l, an, cc);
+                cc = keep ? cn : -l * cn;
+                b0 = keep ? fmaf(-l, b0, b1) : fmaf(-l, b1, b0);
+                a = na;
+            } else {
+                x[k] = b0 * __builtin_amdgcn_rcpf(fabsf(a) < tol ? copysignf(tol, a) : a);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // reload d, e from LDS below rather than keep the forward
+        // loop's copies live across it
+        __asm__ volatile("" ::: "memory");
+        float x1 = 0.0f, x2 = 0.0f;
+        float rnx = s.re[N - 2], dnx2 = s.d[N - 1], enx2 = s.e[N - 1];   // one step ahead
+#pragma unroll
+        for (int k = N - 1; k >= 0; --k) {
+            float xv = x[k];
+            if (k + 1 < N) {
+                const float rk = rnx, dk1 = dnx2, ek1 = enx2;
+                if (k > 0) {
+                    rnx = s.re[k - 1];
+                    dnx2 = s.d[k];
+                    enx2 = s.e[k];
+                }
+                const bool swapped = u[k] != u[k];
+                const float q1 = swapped ? (dk1 - lam) * rk : u[k];
+                const float q2 = swapped ? ek1 * rk : 0.0f;
+                xv = fmaf(-q2, x2, fmaf(-q1, x1, xv));
+            }
+            x[k] = xv;
+            __asm__ volatile("" : "+v"(x[k]));
+            x2 = x1;
+            x1 = xv;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        normalize<N>(x);
+        // modified Gram-Schmidt within each close group, one member per
+        // round: the member at position t is final when round t begins
+        for (int t = 0; t < rounds; ++t) {
+            if (pos == t) normalize<N>(x);
+            const int src = g * N + min(cs + t, N - 1);
+            float dot = 0.0f;
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                u[k] = __shfl(x[k], src, 64);
+                dot = fmaf(u[k], x[k], dot);
+            }
+            if (pos > t) {
+#pragma unroll
+                for (int k = 0; k < N; ++k) x[k] = fmaf(-dot, u[k], x[k]);
+            }
+        }
+        normalize<N>(x);
+    }
+
+    if (diag) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) x[k] = k == row ? 1.0f : 0.0f;
+    }
+
+    // 7. back to A's basis; lane c writes column c of V (over the
+    // reflectors: every lane's loads of them have returned by the last
+    // barrier of the back-transform)
+    {
+        float nx[kBT];
+        const float* vsrc = V + (live ? mat : 0) * per;
+        bt_fetch<N>(nx, vsrc, N - 3, c, nn);
+        backtransform_step<N - 3, N>(x, s, c, nn, vsrc, nx);
+    }
+    if (live && mine) {
+        float* dst = V + mat * per;
+#pragma unroll
+        for (int r = 0; r < N; ++r)
+            if (r < nn) dst[(size_t)r * n + c] = bad ? qnan() : x[r];
+    }
+}
+
+template <int N, bool VEC, bool SPLIT = false>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 1))) void eigh_small_kernel(const float* __restrict__ A, float* __restrict__ W,
                                                         float* __restrict__ V, uint32_t* __restrict__ info,
-                                                        uint32_t batch, uint32_t n, int lower) {
+                                                        uint32_t batch, uint32_t n, int lower,
+                                                        float* __restrict__ Sv) {
     constexpr int MPW = 64 / N;
     __shared__ EighLds<N> lds[MPW];
     const int lane = threadIdx.x;
@@ -251,28 +403,31 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     const int nn = (int)n;
     const size_t per = (size_t)n * n;
 
-    // 1. the read triangle, mirrored into a full symmetric matrix: lane c
-    // loads column c (coalesced) and row c, and takes each entry from the
-    // read triangle.  Every load is unconditional (clamped into the matrix)
-    // so that they are all in flight together.
+    // 1. the read triangle, mirrored into a full symmetric matrix: entry r
+    // of lane c's column comes from the column (coalesced across lanes) in
+    // the read triangle and from row c (served from L2) outside it, one
+    // load per entry.  Every load is unconditional (clamped into the
+    // matrix) so that they are all in flight together.
     float x[N];
     float amax = 0.0f;
     int bad = 0;
     {
         const int cc = c < nn ? c : nn - 1;
         const float* src = A + (live ? mat : 0) * per;
-        float xr[N];
 #pragma unroll
         for (int r = 0; r < N; ++r) {
             const int rr = r < nn ? r : nn - 1;
-            x[r] = src[(size_t)rr * n + cc];
-            xr[r] = src[(size_t)cc * n + rr];
+            const bool take = lower ? r >= c : r <= c;
+            const int off = take ? rr * nn + cc : cc * nn + rr;   // 32-bit: n <= 64
+            x[r] = src[off];
+            // 16 loads at a time: their addresses are not all held at once
+            if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int r = 0; r < N; ++r) {
             const bool in = live && r < nn && c < nn;
             const bool take = lower ? r >= c : r <= c;
-            const float v = in ? (take ? x[r] : xr[r]) : 0.0f;
+            const float v = in ? x[r] : 0.0f;
             amax = fmaxf(amax, fabsf(v));
             bad |= in && take && !finite_f(v);
             x[r] = v;
@@ -408,128 +563,24 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
     if (diag) lam = s.d[row];
 
     if (VEC) {
-        // 5. inverse iteration: T - lam I = P L U with partial pivoting
-        // (slagtf), the right-hand side carried along.  x[k] holds the
-        // right-hand side, then row k of U scaled by its pivot (x, and u =
-        // the superdiagonal entry where row k kept its place), then the
-        // solution.  Where rows k and k+1 were swapped (u = NaN), U's row is
-        // (e_k, d_{k+1} - lam, e_{k+1}), rebuilt from LDS on the way back.
-        // The whole tridiagonal is solved: at a split (e = 0) the
-        // elimination decouples, and rows past n (kPad, e = 0) carry zeros.
-        // Eigenvectors of other blocks with an eigenvalue as close as this
-        // one's fall into its close group below.
-        const float tol = fmaxf(kEps * tnorm, kSafeMin);   // smaller pivots become +-tol
-        float u[N];
-#pragma unroll
-        for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)(mat * 64 + c), (uint32_t)k) : 0.0f;
-        // close eigenvalues: lanes cs .. c with gaps <= kOrtol |T|
-        const float prev = __shfl_up(lam, 1, N);
-        const bool brk = c == 0 || !mine || diag || lam - prev > kOrtol * tnorm;
-        uint64_t brks = __ballot(brk);
-        if (N < 64) brks = (brks >> (g * N)) & ((1ull << N) - 1);
-        const int cs = 63 - __clzll((unsigned long long)(brks & ((2ull << c) - 1)));
-        const int pos = c - cs;
-        int rounds = pos;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
-        for (int pass = 0; pass < (all_diag ? 0 : 2); ++pass) {
-            float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
-            // d and e of the next row are read one step ahead (their LDS
-            // latency hides behind this step's recurrence)
-            float enow = s.e[0], dnx = s.d[1], enx = s.e[1];
-#pragma unroll
-            for (int k = 0; k < N; ++k) {
-                if (k + 1 < N) {
-                    const float ek = enow;
-                    const float an = dnx - lam, cn = enx, b1 = x[k + 1];
-                    enow = enx;
-                    if (k + 2 < N) {
-                        dnx = s.d[k + 2];
-                        enx = s.e[k + 2];
-                    }
-                    const bool keep = fabsf(a) >= fabsf(ek);
-                    const float piv = keep ? a : ek;
-                    const float r0 = __builtin_amdgcn_rcpf(fabsf(piv) < tol ? copysignf(tol, piv) : piv);
-                    const float l = (keep ? ek : a) * r0;
-                    x[k] = (keep ? b0 : b1) * r0;
-                    u[k] = keep ? cc * r0 : qnan();   // NaN marks a swap
-                    // pinned: computed here, not sunk into the backward loop
-                    // with their factors kept live instead
-                    __asm__ volatile("" : "+v"(x[k]), "+v"(u[k]));
-                    const float na = keep ? fmaf(-l, cc, an) : fmaf(-l, an, cc);
-                    cc = keep ? cn : -l * cn;
-                    b0 = keep ? fmaf(-l, b0, b1) : fmaf(-l, b1, b0);
-                    a = na;
-                } else {
-                    x[k] = b0 * __builtin_amdgcn_rcpf(fabsf(a) < tol ? copysignf(tol, a) : a);
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // reload d, e from LDS below rather than keep the forward
-            // loop's copies live across it
-            __asm__ volatile("" ::: "memory");
-            float x1 = 0.0f, x2 = 0.0f;
-            float rnx = s.re[N - 2], dnx2 = s.d[N - 1], enx2 = s.e[N - 1];   // one step ahead
-#pragma unroll
-            for (int k = N - 1; k >= 0; --k) {
-                float xv = x[k];
-                if (k + 1 < N) {
-                    const float rk = rnx, dk1 = dnx2, ek1 = enx2;
-                    if (k > 0) {
-                        rnx = s.re[k - 1];
-                        dnx2 = s.d[k];
-                        enx2 = s.e[k];
-                    }
-                    const bool swapped = u[k] != u[k];
-                    const float q1 = swapped ? (dk1 - lam) * rk : u[k];
-                    const float q2 = swapped ? ek1 * rk : 0.0f;
-                    xv = fmaf(-q2, x2, fmaf(-q1, x1, xv));
-                }
-                x[k] = xv;
-                __asm__ volatile("" : "+v"(x[k]));
-                x2 = x1;
-                x1 = xv;
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            normalize<N>(x);
-            // modified Gram-Schmidt within each close group, one member per
-            // round: the member at position t is final when round t begins
-            for (int t = 0; t < rounds; ++t) {
-                if (pos == t) normalize<N>(x);
-                const int src = g * N + min(cs + t, N - 1);
-                float dot = 0.0f;
-#pragma unroll
-                for (int k = 0; k < N; ++k) {
-                    u[k] = __shfl(x[k], src, 64);
-                    dot = fmaf(u[k], x[k], dot);
-                }
-                if (pos > t) {
-#pragma unroll
-                    for (int k = 0; k < N; ++k) x[k] = fmaf(-dot, u[k], x[k]);
+        if (SPLIT) {
+            // phase A of the split launch: what the vectors need, saved
+            float* st = Sv + mat * kSplitFloats;
+            if (live) {
+                st[c] = s.d[c];
+                st[N + c] = s.e[c];
+                st[2 * N + c] = s.re[c];
+                st[3 * N + c] = c < N - 2 ? s.tau[c] : 0.0f;
+                st[4 * N + c] = lam;
+                st[5 * N + c] = __int_as_float(diag ? row : -1);
+                if (c == 0) {
+                    st[6 * N] = tnorm;
+                    st[6 * N + 1] = __int_as_float(all_diag ? 1 : 0);
+                    st[6 * N + 2] = __int_as_float(bad);
                 }
             }
-            normalize<N>(x);
-        }
-
-        if (diag) {
-#pragma unroll
-            for (int k = 0; k < N; ++k) x[k] = k == row ? 1.0f : 0.0f;
-        }
-
-        // 7. back to A's basis; lane c writes column c of V (over the
-        // reflectors: every lane's loads of them have returned by the last
-        // barrier of the back-transform)
-        {
-            float nx[kBT];
-            const float* vsrc = V + (live ? mat : 0) * per;
-            bt_fetch<N>(nx, vsrc, N - 3, c, nn);
-            backtransform_step<N - 3, N>(x, s, c, nn, vsrc, nx);
-        }
-        if (live && mine) {
-            float* dst = V + mat * per;
-#pragma unroll
-            for (int r = 0; r < N; ++r)
-                if (r < nn) dst[(size_t)r * n + c] = bad ? qnan() : x[r];
+        } else {
+            eigh_vectors<N>(s, x, V, c, g, mat, live, nn, n, per, lam, mine, diag, row, all_diag, tnorm, bad);
         }
     }
     if (live && mine) W[mat * n + c] = bad ? qnan() : ldexpf(lam, ex);
@@ -537,35 +588,79 @@ __global__ __launch_bounds__(64) void eigh_small_kernel(const float* __restrict_
         info[mat] = bad ? (1u << 17) : ((uint32_t)steps | (1u << 16));
 }
 
+// Phase B of the split launch (n = 64 with vectors): stages 5-7 from the
+// state phase A left.
+__global__ __launch_bounds__(64) void eigh_vectors_kernel(const float* __restrict__ Sv, float* __restrict__ V,
+                                                          uint32_t batch, uint32_t n) {
+    constexpr int N = kSplitN;
+    __shared__ EighLds<N> lds[1];
+    EighLds<N>& s = lds[0];
+    const int c = threadIdx.x;
+    const size_t mat = blockIdx.x;
+    const bool live = mat < batch;
+    const int nn = (int)n;
+    const size_t per = (size_t)n * n;
+    const float* st = Sv + (live ? mat : 0) * kSplitFloats;
+    s.d[c] = st[c];
+    s.e[c] = st[N + c];
+    s.re[c] = st[2 * N + c];
+    s.tau[c] = st[3 * N + c];
+    if (c < 4) {
+        s.d[N + c] = kPad;
+        s.e[N + c] = 0.0f;
+        s.re[N + c] = 0.0f;
+    }
+    const float lam = st[4 * N + c];
+    const int rw = __float_as_int(st[5 * N + c]);
+    const float tnorm = st[6 * N];
+    const bool all_diag = __float_as_int(st[6 * N + 1]) != 0;
+    const int bad = __float_as_int(st[6 * N + 2]);
+    wave_lds_sync();
+    float x[N];
+    eigh_vectors<N>(s, x, V, c, 0, mat, live, nn, n, per, lam, c < nn, rw >= 0, rw >= 0 ? rw : c, all_diag, tnorm,
+                    bad);
+}
+
 template <int N, bool VEC>
-void launch(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
+void launch(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
             hipStream_t s) {
     constexpr int MPW = 64 / N;
     KernelTimer t("eigh_small", s);
-    hipLaunchKernelGGL((eigh_small_kernel<N, VEC>), dim3((uint32_t)cdiv(batch, MPW)), dim3(64), 0, s, a, w, v, info,
-                       batch, n, lower ? 1 : 0);
+    if constexpr (N == kSplitN && VEC) {
+        hipLaunchKernelGGL((eigh_small_kernel<N, true, true>), dim3(batch), dim3(64), 0, s, a, w, v, info, batch, n,
+                           lower ? 1 : 0, ws);
+        hipLaunchKernelGGL(eigh_vectors_kernel, dim3(batch), dim3(64), 0, s, ws, v, batch, n);
+    } else {
+        hipLaunchKernelGGL((eigh_small_kernel<N, VEC>), dim3((uint32_t)cdiv(batch, MPW)), dim3(64), 0, s, a, w, v,
+                           info, batch, n, lower ? 1 : 0, ws);
+    }
     t.stop();
 }
 
 template <bool VEC>
-void dispatch(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
+void dispatch(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
               hipStream_t s) {
-    if (n <= 8) launch<8, VEC>(a, w, v, info, batch, n, lower, s);
-    else if (n <= 16) launch<16, VEC>(a, w, v, info, batch, n, lower, s);
-    else if (n <= 32) launch<32, VEC>(a, w, v, info, batch, n, lower, s);
-    else launch<64, VEC>(a, w, v, info, batch, n, lower, s);
+    if (n <= 8) launch<8, VEC>(a, w, v, info, batch, n, lower, ws, s);
+    else if (n <= 16) launch<16, VEC>(a, w, v, info, batch, n, lower, ws, s);
+    else if (n <= 32) launch<32, VEC>(a, w, v, info, batch, n, lower, ws, s);
+    else launch<64, VEC>(a, w, v, info, batch, n, lower, ws, s);
 }
 
 }  // namespace
 
 bool eigh_small_fits(uint32_t n) { return n >= 1 && n <= 64; }
 
-void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
+size_t eigh_small_workspace(uint32_t n, uint32_t batch, bool vectors) {
+    return (vectors && n > 32) ? (size_t)batch * kSplitFloats * sizeof(float) : 0;
+}
+
+void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
                 hipStream_t s) {
     if (!eigh_small_fits(n)) invalid("[eigh] eigh_small takes n <= 64");
     if (batch == 0) return;
-    if (v) dispatch<true>(a, w, v, info, batch, n, lower, s);
-    else dispatch<false>(a, w, nullptr, info, batch, n, lower, s);
+    if (v && n > 32 && !ws) invalid("[eigh] eigh_small needs its workspace for n > 32 with vectors");
+    if (v) dispatch<true>(a, w, v, info, batch, n, lower, ws, s);
+    else dispatch<false>(a, w, nullptr, info, batch, n, lower, ws, s);
     MLA_HIP(hipGetLastError());
 }
 

@@ -59,7 +59,9 @@ void trsm_blocked_one(const float* T, int ldt, float* B, int n, int nrhs, bool u
 
 // ---- symmetric eigendecomposition, n <= 64 ----
 bool eigh_small_fits(uint32_t n);
-void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower,
+// Bytes of device workspace eigh_small needs (0 without vectors or for n <= 32).
+size_t eigh_small_workspace(uint32_t n, uint32_t batch, bool vectors);
+void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
                 hipStream_t s);
 
 // ---- symmetric eigendecomposition for larger n (<= 16384), one matrix at a time ----
