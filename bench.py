@@ -44,7 +44,7 @@ FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
 # x1.9998, WRITE_SIZE x1.0); the runs and the scaling are in
 # profiles/<kernel>_<workload>.md.  Workloads not yet counted report null.
 TRAFFIC_BYTES = {
-    "eigh": 106_810_252 + 97_147_822,  # profiles/eigh_small_eigh.md
+    "eigh": 101_633_352 + 111_206_679,  # profiles/eigh_small_eigh.md
     "qr": 41_840_322 + 81_920_000,     # profiles/qr_small_qr.md
 }
 
@@ -54,7 +54,7 @@ TRAFFIC_BYTES = {
 # occupies its SIMD for 4 cycles; MI355X has 1024 SIMDs at 2.4 GHz.
 VALU_INSTRUCTIONS = {
     "qr": 36_865_000,
-    "eigh": 139_619_150,
+    "eigh": 89_886_238 + 48_865_829,
     "svd": 93_806_592 + 162_341_627 + 51_152_896,
 }
 SIMDS, CLOCK_HZ = 1024, 2.4e9
