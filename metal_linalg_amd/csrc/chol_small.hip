@@ -1,5 +1,5 @@
-// Batched Cholesky of small matrices (n <= 32), one matrix per lane group of
-// a wave64, held in registers.
+// Batched Cholesky of small matrices (n <= 64), one matrix per lane group of
+// a wave64 (a whole wave at 33 <= n <= 64), held in registers.
 //
 // Role: the MI355X counterpart of the reference's chol_simd
 // (reference: shaders/Cholesky.metal:61-146, driver src/cholesky_gpu.mm:216-244)
@@ -102,15 +102,16 @@ void launch(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n
 
 }  // namespace
 
-bool chol_small_fits(uint32_t n) { return n >= 1 && n <= 32; }
+bool chol_small_fits(uint32_t n) { return n >= 1 && n <= 64; }
 
 void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s) {
-    if (!chol_small_fits(n)) invalid("[cholesky] chol_small takes n <= 32");
+    if (!chol_small_fits(n)) invalid("[cholesky] chol_small takes n <= 64");
     if (batch == 0) return;
     if (n <= 4) launch<4>(a, l, info, batch, n, upper, s);
     else if (n <= 8) launch<8>(a, l, info, batch, n, upper, s);
     else if (n <= 16) launch<16>(a, l, info, batch, n, upper, s);
-    else launch<32>(a, l, info, batch, n, upper, s);
+    else if (n <= 32) launch<32>(a, l, info, batch, n, upper, s);
+    else launch<64>(a, l, info, batch, n, upper, s);
     MLA_HIP(hipGetLastError());
 }
 
