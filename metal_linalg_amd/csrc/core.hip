@@ -309,7 +309,7 @@ void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dlu = call.out(lu, (size_t)B * n * n);
     uint32_t* dp = call.out(pivots, (size_t)B * n);
-    if (lu_small_fits(n)) {
+    if (lu_small_factor_fits(n)) {
         uint32_t* di = call.out(info, B);
         lu_small_factor(da, dlu, dp, di, B, n, call.stream());
     } else {

@@ -1,6 +1,6 @@
 // Batched LU with partial pivoting, solve, inverse and triangular solve for
-// small matrices (n <= 32), one matrix per lane group of a wave64, in
-// registers.
+// small matrices (n <= 32; the factorization alone to n = 64, one matrix per
+// wave), one matrix per lane group of a wave64, in registers.
 //
 // Role: the reference has no batched-small GPU LU or TRSM; its CPU path is
 // the contract (reference: src/lu_cpu.mm:72-157, src/trsm.mm:193-206):
@@ -248,7 +248,8 @@ void dispatch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const
     if (n <= 4) launch_lu<4, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if (n <= 8) launch_lu<8, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if (n <= 16) launch_lu<16, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
-    else launch_lu<32, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else if (n <= 32) launch_lu<32, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else if constexpr (MODE == kFactor) launch_lu<64, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     MLA_HIP(hipGetLastError());
 }
 
@@ -267,10 +268,11 @@ constexpr uint32_t kMaxGridY = 65535;
 }  // namespace
 
 bool lu_small_fits(uint32_t n) { return n >= 1 && n <= 32; }
+bool lu_small_factor_fits(uint32_t n) { return n >= 1 && n <= 64; }
 
 void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
                      hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[lu_factor] lu_small takes n <= 32");
+    if (!lu_small_factor_fits(n)) invalid("[lu_factor] lu_small takes n <= 64");
     if (batch == 0) return;
     dispatch_lu<kFactor>(a, lu, pivots, info, nullptr, nullptr, batch, n, 0, s, "lu_small_factor");
 }

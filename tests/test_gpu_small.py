@@ -197,3 +197,25 @@ def test_host_and_device_pointers_agree(cuda, api):
     l1, i1 = api.cholesky(a)
     l2, i2 = api.cholesky(dev(torch, a))
     assert np.array_equal(l1, to_np(l2), equal_nan=True) and np.array_equal(u32(i1), u32(i2))
+
+
+@pytest.mark.parametrize("n", [33, 48, 64])
+def test_lu_factor_one_matrix_per_wave(cuda, api, oracle, n):
+    """33 <= n <= 64: the batched factorization with one matrix per wave; a
+    zero column in one matrix gives LAPACK's info there and nowhere else."""
+    rng = np.random.default_rng(300 + n)
+    a = rng.standard_normal((64, n, n)).astype(np.float32)
+    k = n // 2
+    a[5, :, k - 1] = 0.0
+    lu, piv, info = api.lu_factor(a)
+    lu, piv, info = to_np(lu), u32(piv), u32(info)
+    lo, po, io = oracle.lu_factor(a)
+    assert np.array_equal(info, io) and info[5] == k and np.count_nonzero(info) == 1
+    res = lu_residual(a, lu, piv)
+    assert res.max() <= bound(n), res.max()
+    differ = np.nonzero(np.any(piv != po, axis=-1))[0]
+    for i in differ:
+        assert near_tie(a[i], piv[i], po[i]), i
+    same = np.setdiff1d(np.arange(a.shape[0]), differ)
+    d = np.abs(lu[same] - lo[same]).max(axis=(-2, -1)) / np.abs(lo[same]).max(axis=(-2, -1))
+    assert d.max() <= 1e-3
