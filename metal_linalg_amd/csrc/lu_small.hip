@@ -1,6 +1,6 @@
 // Batched LU with partial pivoting, solve, inverse and triangular solve for
-// small matrices (n <= 32; the factorization alone to n = 64, one matrix per
-// wave), one matrix per lane group of a wave64, in registers.
+// small matrices (n <= 64), one matrix per lane group of a wave64, in
+// registers (a whole wave per matrix at 33 <= n <= 64).
 //
 // Role: the reference has no batched-small GPU LU or TRSM; its CPU path is
 // the contract (reference: src/lu_cpu.mm:72-157, src/trsm.mm:193-206):
@@ -230,6 +230,118 @@ __global__ __launch_bounds__(64) void trsm_small_kernel(const float* __restrict_
         if (r < (int)n) dst[(size_t)r * nrhs + col0 + rc] = y[r];
 }
 
+// 33 <= n <= 64: one matrix per wave, the right-hand sides in LDS.
+// ysh[r][j] holds row r of right-hand side j (lane j reads and writes only
+// its own column, so the substitutions need no synchronisation); the
+// triangle or factor is in LDS by columns (fac[k][r] = LU(r, k)), read as
+// broadcasts.  The loops run to n at run time.  The arithmetic is that of
+// the kernels above: the swaps composed and applied first, then the same
+// multiply-adds and divisions in the same order.
+template <int MODE>
+__global__ __launch_bounds__(64) void lu_wide_kernel(const float* __restrict__ A, uint32_t* __restrict__ info_out,
+                                                     const float* __restrict__ B, float* __restrict__ X,
+                                                     uint32_t n, uint32_t nrhs) {
+    constexpr int N = 64;
+    __shared__ float col[N + 4];
+    __shared__ int pivsh[2 * N];
+    __shared__ int permsh[N];
+    __shared__ float fac[N][N + 1];
+    __shared__ float ysh[N][N + 1];
+    const int c = threadIdx.x;
+    const int nn = (int)n;
+    const size_t mat = blockIdx.x;
+    const int col0 = (int)blockIdx.y * N;
+    const int nr = MODE == kInv ? nn : (int)nrhs;
+    const bool rhs_lane = col0 + c < nr;
+    const size_t per = (size_t)n * n;
+
+    float x[N];
+    const float* src = A + mat * per;
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        float v = (r == c) ? 1.0f : 0.0f;   // identity padding
+        if (c < nn && r < nn) v = src[(size_t)r * n + c];
+        x[r] = v;
+    }
+    int info = 0, mypiv = 0;
+    lu_step<0, N>(x, col, pivsh, c, nn, info, mypiv);
+#pragma unroll
+    for (int r = 0; r < N; ++r) fac[c][r] = x[r];
+    // lane r ends with the source row of position r: the swaps of the
+    // pivots, in order, exchanged between lanes k and p
+    int src_row = c;
+    for (int k = 0; k < nn; ++k) {
+        const int p = pivsh[k];
+        const int from_p = __shfl(src_row, p, 64);
+        const int from_k = __shfl(src_row, k, 64);
+        src_row = c == k ? from_p : (c == p ? from_k : src_row);
+    }
+    permsh[c] = src_row;
+    wave_lds_sync();
+    const float* bsrc = MODE == kInv ? nullptr : B + mat * (size_t)n * nr;
+    for (int r = 0; r < nn; ++r) {
+        const int sr = permsh[r];
+        float v = 0.0f;
+        if (rhs_lane) v = MODE == kInv ? (sr == col0 + c ? 1.0f : 0.0f) : bsrc[(size_t)sr * nr + col0 + c];
+        ysh[r][c] = v;
+    }
+    for (int k = 0; k < nn; ++k) {   // unit lower L
+        const float yk = ysh[k][c];
+        for (int r = k + 1; r < nn; ++r) ysh[r][c] = fmaf(-fac[k][r], yk, ysh[r][c]);
+    }
+    for (int k = nn - 1; k >= 0; --k) {   // U
+        const float v = ysh[k][c] / fac[k][k];
+        ysh[k][c] = v;
+        for (int r = 0; r < k; ++r) ysh[r][c] = fmaf(-fac[k][r], v, ysh[r][c]);
+    }
+    if (info_out && c == 0 && blockIdx.y == 0) info_out[mat] = (uint32_t)info;
+    if (!rhs_lane) return;
+    float* dst = X + mat * (size_t)n * nr;
+    for (int r = 0; r < nn; ++r) dst[(size_t)r * nr + col0 + c] = info ? qnan() : ysh[r][c];
+}
+
+__global__ __launch_bounds__(64) void trsm_wide_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                       float* __restrict__ X, uint32_t n, uint32_t nrhs, int upper,
+                                                       int unit) {
+    constexpr int N = 64;
+    __shared__ float tsh[N][N + 1];   // tsh[k][r] = T(r, k)
+    __shared__ float ysh[N][N + 1];
+    const int c = threadIdx.x;
+    const int nn = (int)n;
+    const size_t mat = blockIdx.x;
+    const int col0 = (int)blockIdx.y * N;
+    const bool rhs_lane = col0 + c < (int)nrhs;
+    const float* src = A + mat * (size_t)n * n;
+    const float* bsrc = B + mat * (size_t)n * nrhs;
+    for (int r = 0; r < nn; ++r) {
+        float v = 0.0f;
+        if (c < nn) {
+            const bool in = upper ? r < c : r > c;   // strictly inside the triangle
+            if (in) v = src[(size_t)r * n + c];
+            else if (r == c) v = unit ? 1.0f : src[(size_t)r * n + c];
+        }
+        tsh[c][r] = v;
+        ysh[r][c] = rhs_lane ? bsrc[(size_t)r * nrhs + col0 + c] : 0.0f;
+    }
+    wave_lds_sync();
+    if (upper) {
+        for (int k = nn - 1; k >= 0; --k) {
+            const float v = ysh[k][c] / tsh[k][k];
+            ysh[k][c] = v;
+            for (int r = 0; r < k; ++r) ysh[r][c] = fmaf(-tsh[k][r], v, ysh[r][c]);
+        }
+    } else {
+        for (int k = 0; k < nn; ++k) {
+            const float v = ysh[k][c] / tsh[k][k];
+            ysh[k][c] = v;
+            for (int r = k + 1; r < nn; ++r) ysh[r][c] = fmaf(-tsh[k][r], v, ysh[r][c]);
+        }
+    }
+    if (!rhs_lane) return;
+    float* dst = X + mat * (size_t)n * nrhs;
+    for (int r = 0; r < nn; ++r) dst[(size_t)r * nrhs + col0 + c] = ysh[r][c];
+}
+
 template <int N, int MODE>
 void launch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const float* b, float* x, uint32_t batch,
                uint32_t n, uint32_t nrhs, hipStream_t s, const char* name) {
@@ -250,6 +362,12 @@ void dispatch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const
     else if (n <= 16) launch_lu<16, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if (n <= 32) launch_lu<32, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if constexpr (MODE == kFactor) launch_lu<64, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
+    else {
+        const uint32_t chunks = MODE == kSolve ? (uint32_t)cdiv(nrhs, 64) : 1;
+        KernelTimer t(name, s);
+        hipLaunchKernelGGL((lu_wide_kernel<MODE>), dim3(batch, chunks), dim3(64), 0, s, a, info, b, x, n, nrhs);
+        t.stop();
+    }
     MLA_HIP(hipGetLastError());
 }
 
@@ -267,7 +385,7 @@ constexpr uint32_t kMaxGridY = 65535;
 
 }  // namespace
 
-bool lu_small_fits(uint32_t n) { return n >= 1 && n <= 32; }
+bool lu_small_fits(uint32_t n) { return n >= 1 && n <= 64; }
 bool lu_small_factor_fits(uint32_t n) { return n >= 1 && n <= 64; }
 
 void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
@@ -279,29 +397,35 @@ void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info
 
 void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, uint32_t batch,
                     uint32_t n, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[solve] lu_small takes n <= 32");
+    if (!lu_small_fits(n)) invalid("[solve] lu_small takes n <= 64");
     if (batch == 0 || nrhs == 0) return;
-    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : 32;
+    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64;
     if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve] too many right-hand sides for one call");
     dispatch_lu<kSolve>(a, nullptr, nullptr, info, b, x, batch, n, nrhs, s, "lu_small_solve");
 }
 
 void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint32_t n, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[inv] lu_small takes n <= 32");
+    if (!lu_small_fits(n)) invalid("[inv] lu_small takes n <= 64");
     if (batch == 0) return;
     dispatch_lu<kInv>(a, nullptr, nullptr, info, nullptr, x, batch, n, n, s, "lu_small_inv");
 }
 
 void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
                 bool unit, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[solve_triangular] trsm_small takes n <= 32");
+    if (!lu_small_fits(n)) invalid("[solve_triangular] trsm_small takes n <= 64");
     if (batch == 0 || nrhs == 0) return;
-    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : 32;
+    const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64;
     if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve_triangular] too many right-hand sides for one call");
     if (n <= 4) launch_trsm<4>(a, b, x, batch, n, nrhs, upper, unit, s);
     else if (n <= 8) launch_trsm<8>(a, b, x, batch, n, nrhs, upper, unit, s);
     else if (n <= 16) launch_trsm<16>(a, b, x, batch, n, nrhs, upper, unit, s);
-    else launch_trsm<32>(a, b, x, batch, n, nrhs, upper, unit, s);
+    else if (n <= 32) launch_trsm<32>(a, b, x, batch, n, nrhs, upper, unit, s);
+    else {
+        KernelTimer t("trsm_small", s);
+        hipLaunchKernelGGL(trsm_wide_kernel, dim3(batch, (uint32_t)cdiv(nrhs, N)), dim3(64), 0, s, a, b, x, n, nrhs,
+                           upper ? 1 : 0, unit ? 1 : 0);
+        t.stop();
+    }
     MLA_HIP(hipGetLastError());
 }
 

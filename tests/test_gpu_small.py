@@ -138,8 +138,8 @@ def test_config4_lu_solve_trsm(cuda, api, oracle):
     assert (np.abs(z - zo).max(axis=(-2, -1)) / np.abs(zo).max(axis=(-2, -1))).max() <= 1e-3
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 7, 8, 16, 23, 32])
-@pytest.mark.parametrize("nrhs", [1, 4, 17, 40])
+@pytest.mark.parametrize("n", [1, 2, 3, 7, 8, 16, 23, 32, 33, 50, 64])
+@pytest.mark.parametrize("nrhs", [1, 4, 17, 40, 70])
 def test_solve_shapes(cuda, api, oracle, n, nrhs):
     a = gaussian((40, n, n), seed=n * 7 + nrhs) + np.float32(2 * n) * np.eye(n, dtype=np.float32)
     b = gaussian((40, n, nrhs), seed=nrhs)
@@ -163,7 +163,7 @@ def test_solve_shapes(cuda, api, oracle, n, nrhs):
             assert (np.abs(y - yo).max(axis=(-2, -1)) / np.abs(yo).max(axis=(-2, -1))).max() <= 1e-4
 
 
-@pytest.mark.parametrize("n", [1, 2, 5, 16, 32])
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 32, 33, 64])
 def test_lu_inv_shapes(cuda, api, oracle, n):
     a = gaussian((60, n, n), seed=n + 100)
     lu, piv, info = api.lu_factor(a)
@@ -176,10 +176,11 @@ def test_lu_inv_shapes(cuda, api, oracle, n):
     assert e.max() <= bound(n)
 
 
-def test_singular_lu_gives_nan_for_that_matrix(cuda, api, oracle):
-    a = gaussian((3, 5, 5), seed=41)
+@pytest.mark.parametrize("n", [5, 40])
+def test_singular_lu_gives_nan_for_that_matrix(cuda, api, oracle, n):
+    a = gaussian((3, n, n), seed=41)
     a[1, :, 2] = 0.0
-    b = gaussian((3, 5, 2), seed=42)
+    b = gaussian((3, n, 2), seed=42)
     lu, piv, info = api.lu_factor(a)
     assert np.array_equal(u32(info), oracle.lu_factor(a)[2]) and u32(info)[1] == 3
     x, info = api.solve(a, b)
