@@ -62,7 +62,7 @@ def test_config5_cholesky(cuda, api, oracle):
     assert np.all(np.triu(l, 1) == 0)
 
 
-# ---- LU, solve, inverse, triangular solve (n > 32: the blocked path) ----
+# ---- LU, solve, inverse, triangular solve (n > 64: the blocked path; 33 and 64 run the one-wave kernels) ----
 
 LU_SIZES = [33, 64, 100, 128, 129, 200, 300, 512]
 
