@@ -1,5 +1,6 @@
 // Batched Cholesky of small matrices (n <= 64), one matrix per lane group of
-// a wave64 (a whole wave at 33 <= n <= 64), held in registers.
+// a wave64 (a whole wave at 33 <= n <= 64), held in registers; 65 <= n <= 128
+// one matrix per workgroup in LDS.
 //
 // Role: the MI355X counterpart of the reference's chol_simd
 // (reference: shaders/Cholesky.metal:61-146, driver src/cholesky_gpu.mm:216-244)
@@ -91,6 +92,62 @@ __global__ __launch_bounds__(64) void chol_small_kernel(const float* __restrict_
     }
 }
 
+// 65 <= n <= 128: one matrix per 256-thread workgroup, the lower triangle in
+// LDS (row stride n + 1, 66 KB at n = 128: two workgroups per CU),
+// right-looking with the same arithmetic as above: the pivot's square root,
+// the column times its reciprocal, the rank-1 update of the trailing lower
+// triangle.  The first pivot that is not positive and finite ends the loop
+// in every thread at once (all read the same LDS word) and sets info.
+constexpr int kMidN = 128;
+
+__global__ __launch_bounds__(256) void chol_mid_kernel(const float* __restrict__ A, float* __restrict__ L,
+                                                       uint32_t* __restrict__ info, uint32_t n, int upper) {
+    __shared__ float a[kMidN * (kMidN + 1)];
+    __shared__ int fail_sh;
+    const int t = threadIdx.x;
+    const int nn = (int)n, ld = nn + 1;
+    const size_t mat = blockIdx.x;
+    const float* src = A + mat * (size_t)n * n;
+    for (int i = t; i < nn * nn; i += 256) {
+        const int r = i / nn, c = i - r * nn;
+        if (r >= c) a[r * ld + c] = upper ? src[(size_t)c * n + r] : src[(size_t)r * n + c];
+    }
+    if (t == 0) fail_sh = 0;
+    __syncthreads();
+    for (int k = 0; k < nn; ++k) {
+        const float d = a[k * ld + k];
+        if (!(d > 0.0f && d <= FLT_MAX)) {
+            if (t == 0) fail_sh = k + 1;
+            break;
+        }
+        const float lkk = sqrtf(d);
+        const float inv = 1.0f / lkk;
+        __syncthreads();   // every thread has read the pivot
+        if (t == 0) a[k * ld + k] = lkk;
+        for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] *= inv;
+        __syncthreads();
+        const int m = nn - k - 1;
+        for (int idx = t; idx < m * m; idx += 256) {
+            const int i = idx / m, j = idx - i * m;
+            if (j <= i) {
+                const int r = k + 1 + i, c = k + 1 + j;
+                a[r * ld + c] = fmaf(-a[r * ld + k], a[c * ld + k], a[r * ld + c]);
+            }
+        }
+        __syncthreads();
+    }
+    __syncthreads();
+    const int fail = fail_sh;
+    if (t == 0 && info) info[mat] = (uint32_t)fail;
+    float* dst = L + mat * (size_t)n * n;
+    for (int i = t; i < nn * nn; i += 256) {
+        const int r = i / nn, c = i - r * nn;
+        const float v = fail ? qnan() : (r >= c ? a[r * ld + c] : 0.0f);
+        if (upper) dst[(size_t)c * n + r] = v;   // U = L^T
+        else dst[(size_t)r * n + c] = v;
+    }
+}
+
 template <int N>
 void launch(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s) {
     constexpr int MPW = 64 / N;
@@ -102,16 +159,21 @@ void launch(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n
 
 }  // namespace
 
-bool chol_small_fits(uint32_t n) { return n >= 1 && n <= 64; }
+bool chol_small_fits(uint32_t n) { return n >= 1 && n <= (uint32_t)kMidN; }
 
 void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s) {
-    if (!chol_small_fits(n)) invalid("[cholesky] chol_small takes n <= 64");
+    if (!chol_small_fits(n)) invalid("[cholesky] chol_small takes n <= 128");
     if (batch == 0) return;
     if (n <= 4) launch<4>(a, l, info, batch, n, upper, s);
     else if (n <= 8) launch<8>(a, l, info, batch, n, upper, s);
     else if (n <= 16) launch<16>(a, l, info, batch, n, upper, s);
     else if (n <= 32) launch<32>(a, l, info, batch, n, upper, s);
-    else launch<64>(a, l, info, batch, n, upper, s);
+    else if (n <= 64) launch<64>(a, l, info, batch, n, upper, s);
+    else {
+        KernelTimer t("chol_small", s);
+        hipLaunchKernelGGL(chol_mid_kernel, dim3(batch), dim3(256), 0, s, a, l, info, n, upper ? 1 : 0);
+        t.stop();
+    }
     MLA_HIP(hipGetLastError());
 }
 

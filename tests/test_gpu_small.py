@@ -40,7 +40,7 @@ def test_config4_cholesky(cuda, api, oracle):
     assert d.max() <= bound(16)
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 13, 16, 17, 31, 32, 33, 47, 64])
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 13, 16, 17, 31, 32, 33, 47, 64, 65, 100, 128])
 @pytest.mark.parametrize("upper", [False, True])
 def test_cholesky_shapes(cuda, api, oracle, n, upper):
     rng = np.random.default_rng(n)
@@ -58,7 +58,7 @@ def test_cholesky_shapes(cuda, api, oracle, n, upper):
     assert np.all(other == 0)
 
 
-@pytest.mark.parametrize("n", [16, 64])
+@pytest.mark.parametrize("n", [16, 64, 100])
 def test_cholesky_info_minors(cuda, api, oracle, n):
     rng = np.random.default_rng(4)
     bm = rng.standard_normal((3, n, n)).astype(np.float32)
