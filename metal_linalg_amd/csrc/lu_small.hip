@@ -342,6 +342,103 @@ __global__ __launch_bounds__(64) void trsm_wide_kernel(const float* __restrict__
     for (int r = 0; r < nn; ++r) dst[(size_t)r * nrhs + col0 + c] = ysh[r][c];
 }
 
+// 65 <= n <= 128, the factorization alone: one matrix per 256-thread
+// workgroup, the matrix in LDS (row stride n + 1, 66 KB at n = 128: two
+// workgroups per CU).  Per column: the pivot by a tree over the threads that
+// keeps isamax's answer (the first row of largest magnitude, the diagonal
+// row winning ties and when it holds NaN), the full-row swap, the
+// multipliers and the rank-1 update, as in the kernels above.
+constexpr int kMidN = 128;
+
+__device__ __forceinline__ void piv_take(float& b, int& i, float ob, int oi, int k) {
+    bool take;
+    if (i == k) take = ob > b;           // the diagonal row keeps ties and NaN
+    else if (oi == k) take = !(b > ob);  // unless strictly exceeded
+    else take = ob > b || (ob == b && oi < i);
+    if (take) {
+        b = ob;
+        i = oi;
+    }
+}
+
+__global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A, float* __restrict__ LU,
+                                                     uint32_t* __restrict__ pivots, uint32_t* __restrict__ info_out,
+                                                     uint32_t n) {
+    __shared__ float a[kMidN * (kMidN + 1)];
+    __shared__ float wb[4];
+    __shared__ int wi[4];
+    __shared__ int piv_sh[kMidN];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int nn = (int)n, ld = nn + 1;
+    const size_t mat = blockIdx.x;
+    const float* src = A + mat * (size_t)n * n;
+    for (int e = t; e < nn * nn; e += 256) {
+        const int r = e / nn, c = e - r * nn;
+        a[r * ld + c] = src[e];
+    }
+    __syncthreads();
+    int info = 0;
+    for (int k = 0; k < nn; ++k) {
+        float b = -1.0f;
+        int bi = 0x7fffffff;
+        for (int r = k + t; r < nn; r += 256) {
+            const float v = fabsf(a[r * ld + k]);
+            if (r == k || v > b) {
+                b = v;
+                bi = r;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ob = __shfl_xor(b, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            piv_take(b, bi, ob, oi, k);
+        }
+        if (lane == 0) {
+            wb[wv] = b;
+            wi[wv] = bi;
+        }
+        __syncthreads();
+        if (t == 0) {
+            for (int q = 1; q < 4; ++q) piv_take(b, bi, wb[q], wi[q], k);
+            piv_sh[k] = bi;
+        }
+        __syncthreads();
+        const int p = piv_sh[k];
+        if (p != k)
+            for (int c = t; c < nn; c += 256) {
+                const float x = a[k * ld + c];
+                a[k * ld + c] = a[p * ld + c];
+                a[p * ld + c] = x;
+            }
+        __syncthreads();
+        const float piv = a[k * ld + k];
+        if (piv == 0.0f) {
+            if (info == 0) info = k + 1;
+        } else if (fabsf(piv) >= kSfmin) {
+            const float inv = 1.0f / piv;
+            for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] *= inv;
+        } else {
+            for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] /= piv;
+        }
+        __syncthreads();
+        const int m = nn - k - 1;
+        for (int e = t; e < m * m; e += 256) {
+            const int i = e / m, j = e - i * m;
+            const int r = k + 1 + i, c = k + 1 + j;
+            a[r * ld + c] = fmaf(-a[r * ld + k], a[k * ld + c], a[r * ld + c]);
+        }
+        __syncthreads();
+    }
+    if (t == 0 && info_out) info_out[mat] = (uint32_t)info;
+    for (int k = t; k < nn; k += 256) pivots[mat * n + k] = (uint32_t)piv_sh[k];
+    float* dst = LU + mat * (size_t)n * n;
+    for (int e = t; e < nn * nn; e += 256) {
+        const int r = e / nn, c = e - r * nn;
+        dst[e] = a[r * ld + c];
+    }
+}
+
 template <int N, int MODE>
 void launch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const float* b, float* x, uint32_t batch,
                uint32_t n, uint32_t nrhs, hipStream_t s, const char* name) {
@@ -386,12 +483,19 @@ constexpr uint32_t kMaxGridY = 65535;
 }  // namespace
 
 bool lu_small_fits(uint32_t n) { return n >= 1 && n <= 64; }
-bool lu_small_factor_fits(uint32_t n) { return n >= 1 && n <= 64; }
+bool lu_small_factor_fits(uint32_t n) { return n >= 1 && n <= (uint32_t)kMidN; }
 
 void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
                      hipStream_t s) {
-    if (!lu_small_factor_fits(n)) invalid("[lu_factor] lu_small takes n <= 64");
+    if (!lu_small_factor_fits(n)) invalid("[lu_factor] lu_small takes n <= 128");
     if (batch == 0) return;
+    if (n > 64) {
+        KernelTimer t("lu_small_factor", s);
+        hipLaunchKernelGGL(lu_mid_kernel, dim3(batch), dim3(256), 0, s, a, lu, pivots, info, n);
+        t.stop();
+        MLA_HIP(hipGetLastError());
+        return;
+    }
     dispatch_lu<kFactor>(a, lu, pivots, info, nullptr, nullptr, batch, n, 0, s, "lu_small_factor");
 }
 

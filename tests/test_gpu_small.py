@@ -200,10 +200,11 @@ def test_host_and_device_pointers_agree(cuda, api):
     assert np.array_equal(l1, to_np(l2), equal_nan=True) and np.array_equal(u32(i1), u32(i2))
 
 
-@pytest.mark.parametrize("n", [33, 48, 64])
+@pytest.mark.parametrize("n", [33, 48, 64, 65, 100, 128])
 def test_lu_factor_one_matrix_per_wave(cuda, api, oracle, n):
-    """33 <= n <= 64: the batched factorization with one matrix per wave; a
-    zero column in one matrix gives LAPACK's info there and nowhere else."""
+    """33 <= n <= 128: the batched factorization with one matrix per wave
+    (n <= 64) or per workgroup; a zero column in one matrix gives LAPACK's
+    info there and nowhere else."""
     rng = np.random.default_rng(300 + n)
     a = rng.standard_normal((64, n, n)).astype(np.float32)
     k = n // 2
