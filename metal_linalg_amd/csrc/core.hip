@@ -379,7 +379,7 @@ void solve_triangular(const Matrices& a, const float* b, uint32_t nrhs, bool upp
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    if (lu_small_fits(n)) {
+    if (lu_small_factor_fits(n)) {   // the triangular solve takes the same n
         trsm_small(da, db, dx, B, n, nrhs, upper, unit, call.stream());
     } else {
         if (dx != db)

@@ -300,12 +300,15 @@ __global__ __launch_bounds__(64) void lu_wide_kernel(const float* __restrict__ A
     for (int r = 0; r < nn; ++r) dst[(size_t)r * nr + col0 + c] = info ? qnan() : ysh[r][c];
 }
 
+// NMAX = 64 or 128 (the triangle's columns c and c + 64 loaded by lane c);
+// 64 right-hand sides per workgroup either way.
+template <int NMAX>
 __global__ __launch_bounds__(64) void trsm_wide_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                        float* __restrict__ X, uint32_t n, uint32_t nrhs, int upper,
                                                        int unit) {
     constexpr int N = 64;
-    __shared__ float tsh[N][N + 1];   // tsh[k][r] = T(r, k)
-    __shared__ float ysh[N][N + 1];
+    __shared__ float tsh[NMAX][NMAX + 1];   // tsh[k][r] = T(r, k)
+    __shared__ float ysh[NMAX][N + 1];
     const int c = threadIdx.x;
     const int nn = (int)n;
     const size_t mat = blockIdx.x;
@@ -314,13 +317,17 @@ __global__ __launch_bounds__(64) void trsm_wide_kernel(const float* __restrict__
     const float* src = A + mat * (size_t)n * n;
     const float* bsrc = B + mat * (size_t)n * nrhs;
     for (int r = 0; r < nn; ++r) {
-        float v = 0.0f;
-        if (c < nn) {
-            const bool in = upper ? r < c : r > c;   // strictly inside the triangle
-            if (in) v = src[(size_t)r * n + c];
-            else if (r == c) v = unit ? 1.0f : src[(size_t)r * n + c];
+#pragma unroll
+        for (int h = 0; h < NMAX / N; ++h) {
+            const int cc = c + h * N;
+            float v = 0.0f;
+            if (cc < nn) {
+                const bool in = upper ? r < cc : r > cc;   // strictly inside the triangle
+                if (in) v = src[(size_t)r * n + cc];
+                else if (r == cc) v = unit ? 1.0f : src[(size_t)r * n + cc];
+            }
+            tsh[cc][r] = v;
         }
-        tsh[c][r] = v;
         ysh[r][c] = rhs_lane ? bsrc[(size_t)r * nrhs + col0 + c] : 0.0f;
     }
     wave_lds_sync();
@@ -516,7 +523,7 @@ void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint
 
 void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32_t n, uint32_t nrhs, bool upper,
                 bool unit, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[solve_triangular] trsm_small takes n <= 64");
+    if (!lu_small_factor_fits(n)) invalid("[solve_triangular] trsm_small takes n <= 128");
     if (batch == 0 || nrhs == 0) return;
     const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64;
     if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve_triangular] too many right-hand sides for one call");
@@ -526,8 +533,12 @@ void trsm_small(const float* a, const float* b, float* x, uint32_t batch, uint32
     else if (n <= 32) launch_trsm<32>(a, b, x, batch, n, nrhs, upper, unit, s);
     else {
         KernelTimer t("trsm_small", s);
-        hipLaunchKernelGGL(trsm_wide_kernel, dim3(batch, (uint32_t)cdiv(nrhs, N)), dim3(64), 0, s, a, b, x, n, nrhs,
-                           upper ? 1 : 0, unit ? 1 : 0);
+        if (n <= 64)
+            hipLaunchKernelGGL(trsm_wide_kernel<64>, dim3(batch, (uint32_t)cdiv(nrhs, 64)), dim3(64), 0, s, a, b, x,
+                               n, nrhs, upper ? 1 : 0, unit ? 1 : 0);
+        else
+            hipLaunchKernelGGL(trsm_wide_kernel<kMidN>, dim3(batch, (uint32_t)cdiv(nrhs, 64)), dim3(64), 0, s, a, b,
+                               x, n, nrhs, upper ? 1 : 0, unit ? 1 : 0);
         t.stop();
     }
     MLA_HIP(hipGetLastError());

@@ -221,3 +221,26 @@ def test_lu_factor_one_matrix_per_wave(cuda, api, oracle, n):
     same = np.setdiff1d(np.arange(a.shape[0]), differ)
     d = np.abs(lu[same] - lo[same]).max(axis=(-2, -1)) / np.abs(lo[same]).max(axis=(-2, -1))
     assert d.max() <= 1e-3
+
+
+@pytest.mark.parametrize("n,nrhs", [(65, 3), (100, 70), (128, 8)])
+@pytest.mark.parametrize("upper", [False, True])
+@pytest.mark.parametrize("unit", [False, True])
+def test_solve_triangular_one_workgroup(cuda, api, oracle, n, nrhs, upper, unit):
+    """65 <= n <= 128: the triangle and the right-hand sides in LDS; the
+    other triangle (and a unit diagonal) hold NaN and must not be read."""
+    # off-diagonal entries of size 1/n keep the unit-diagonal triangles well
+    # conditioned at this n (N(0,1) entries grow the solution exponentially)
+    a = (gaussian((24, n, n), seed=n + nrhs) / np.float32(n) + np.float32(2) * np.eye(n, dtype=np.float32)).astype(
+        np.float32)
+    b = gaussian((24, n, nrhs), seed=nrhs + 1)
+    junk = a.copy()
+    iu = np.tril_indices(n, -1) if upper else np.triu_indices(n, 1)
+    junk[:, iu[0], iu[1]] = np.nan
+    if unit:
+        junk[:, np.arange(n), np.arange(n)] = np.nan
+    y = api.solve_triangular(junk, b, upper, unit)
+    yo = oracle.solve_triangular(a, b, upper, unit)
+    assert not np.isnan(y).any()
+    assert (np.abs(y - yo).max(axis=(-2, -1)) / np.abs(yo).max(axis=(-2, -1))).max() <= 1e-4
+
