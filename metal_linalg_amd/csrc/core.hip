@@ -338,7 +338,7 @@ void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t*
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    if (lu_small_fits(n)) {
+    if (lu_small_factor_fits(n)) {
         uint32_t* di = call.out(info, B);
         lu_small_solve(da, db, nrhs, dx, di, B, n, call.stream());
     } else {
@@ -358,7 +358,7 @@ void inv(const Matrices& a, float* x, uint32_t* info) {
     Call call;
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dx = call.out(x, (size_t)B * n * n);
-    if (lu_small_fits(n)) {
+    if (lu_small_factor_fits(n)) {
         uint32_t* di = call.out(info, B);
         lu_small_inv(da, dx, di, B, n, call.stream());
     } else {

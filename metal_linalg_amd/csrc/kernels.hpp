@@ -36,7 +36,7 @@ void chol_blocked(const float* a, float* l, uint32_t* info, float* work, float* 
 
 // ---- LU, solve, inverse, triangular solve, n <= 32 ----
 bool lu_small_fits(uint32_t n);
-bool lu_small_factor_fits(uint32_t n);   // the factorization and the triangular solve: n <= 128
+bool lu_small_factor_fits(uint32_t n);   // factor, solve, inverse, triangular solve: n <= 128
 void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info, uint32_t batch, uint32_t n,
                      hipStream_t s);
 void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, uint32_t batch,

@@ -368,13 +368,22 @@ __device__ __forceinline__ void piv_take(float& b, int& i, float ob, int oi, int
     }
 }
 
+// Solve and inverse (MODE != kFactor) go on in the same workgroup: the swaps
+// composed into one row permutation, 64 right-hand sides gathered through
+// it into LDS (blockIdx.y picks which 64), and the first wave substitutes,
+// one right-hand side per lane, in the order of the kernels above.
+template <int MODE>
 __global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A, float* __restrict__ LU,
                                                      uint32_t* __restrict__ pivots, uint32_t* __restrict__ info_out,
-                                                     uint32_t n) {
+                                                     const float* __restrict__ B, float* __restrict__ X, uint32_t n,
+                                                     uint32_t nrhs) {
+    constexpr int YR = MODE == kFactor ? 1 : kMidN;
     __shared__ float a[kMidN * (kMidN + 1)];
     __shared__ float wb[4];
     __shared__ int wi[4];
     __shared__ int piv_sh[kMidN];
+    __shared__ int perm[YR];
+    __shared__ float ysh[YR][65];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int nn = (int)n, ld = nn + 1;
     const size_t mat = blockIdx.x;
@@ -437,12 +446,57 @@ __global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A
         }
         __syncthreads();
     }
-    if (t == 0 && info_out) info_out[mat] = (uint32_t)info;
-    for (int k = t; k < nn; k += 256) pivots[mat * n + k] = (uint32_t)piv_sh[k];
-    float* dst = LU + mat * (size_t)n * n;
-    for (int e = t; e < nn * nn; e += 256) {
-        const int r = e / nn, c = e - r * nn;
-        dst[e] = a[r * ld + c];
+    if constexpr (MODE == kFactor) {
+        if (t == 0 && info_out) info_out[mat] = (uint32_t)info;
+        for (int k = t; k < nn; k += 256) pivots[mat * n + k] = (uint32_t)piv_sh[k];
+        float* dst = LU + mat * (size_t)n * n;
+        for (int e = t; e < nn * nn; e += 256) {
+            const int r = e / nn, c = e - r * nn;
+            dst[e] = a[r * ld + c];
+        }
+    } else {
+        for (int r = t; r < nn; r += 256) perm[r] = r;
+        __syncthreads();
+        if (t == 0)
+            for (int k = 0; k < nn; ++k) {   // position r of P b is row perm[r] of b
+                const int p = piv_sh[k];
+                const int x = perm[k];
+                perm[k] = perm[p];
+                perm[p] = x;
+            }
+        __syncthreads();
+        const int col0 = (int)blockIdx.y * 64;
+        const int nr = MODE == kInv ? nn : (int)nrhs;
+        const float* bsrc = MODE == kInv ? nullptr : B + mat * (size_t)n * nr;
+        for (int e = t; e < nn * 64; e += 256) {
+            const int r = e >> 6, j = e & 63;
+            float v = 0.0f;
+            if (col0 + j < nr) {
+                const int sr = perm[r];
+                v = MODE == kInv ? (sr == col0 + j ? 1.0f : 0.0f) : bsrc[(size_t)sr * nr + col0 + j];
+            }
+            ysh[r][j] = v;
+        }
+        __syncthreads();
+        if (t < 64) {
+            const int j = t;
+            for (int k = 0; k < nn; ++k) {   // unit lower L
+                const float yk = ysh[k][j];
+                for (int r = k + 1; r < nn; ++r) ysh[r][j] = fmaf(-a[r * ld + k], yk, ysh[r][j]);
+            }
+            for (int k = nn - 1; k >= 0; --k) {   // U
+                const float v = ysh[k][j] / a[k * ld + k];
+                ysh[k][j] = v;
+                for (int r = 0; r < k; ++r) ysh[r][j] = fmaf(-a[r * ld + k], v, ysh[r][j]);
+            }
+        }
+        __syncthreads();
+        if (t == 0 && info_out && blockIdx.y == 0) info_out[mat] = (uint32_t)info;
+        float* dst = X + mat * (size_t)n * nr;
+        for (int e = t; e < nn * 64; e += 256) {
+            const int r = e >> 6, j = e & 63;
+            if (col0 + j < nr) dst[(size_t)r * nr + col0 + j] = info ? qnan() : ysh[r][j];
+        }
     }
 }
 
@@ -466,10 +520,16 @@ void dispatch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const
     else if (n <= 16) launch_lu<16, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if (n <= 32) launch_lu<32, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
     else if constexpr (MODE == kFactor) launch_lu<64, MODE>(a, lu, piv, info, b, x, batch, n, nrhs, s, name);
-    else {
+    else if (n <= 64) {
         const uint32_t chunks = MODE == kSolve ? (uint32_t)cdiv(nrhs, 64) : 1;
         KernelTimer t(name, s);
         hipLaunchKernelGGL((lu_wide_kernel<MODE>), dim3(batch, chunks), dim3(64), 0, s, a, info, b, x, n, nrhs);
+        t.stop();
+    } else {
+        const uint32_t chunks = (uint32_t)cdiv(MODE == kSolve ? nrhs : n, 64);
+        KernelTimer t(name, s);
+        hipLaunchKernelGGL((lu_mid_kernel<MODE>), dim3(batch, chunks), dim3(256), 0, s, a, nullptr, nullptr, info, b,
+                           x, n, nrhs);
         t.stop();
     }
     MLA_HIP(hipGetLastError());
@@ -498,7 +558,8 @@ void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info
     if (batch == 0) return;
     if (n > 64) {
         KernelTimer t("lu_small_factor", s);
-        hipLaunchKernelGGL(lu_mid_kernel, dim3(batch), dim3(256), 0, s, a, lu, pivots, info, n);
+        hipLaunchKernelGGL(lu_mid_kernel<kFactor>, dim3(batch), dim3(256), 0, s, a, lu, pivots, info, nullptr,
+                           nullptr, n, 0u);
         t.stop();
         MLA_HIP(hipGetLastError());
         return;
@@ -508,7 +569,7 @@ void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info
 
 void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uint32_t* info, uint32_t batch,
                     uint32_t n, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[solve] lu_small takes n <= 64");
+    if (!lu_small_factor_fits(n)) invalid("[solve] lu_small takes n <= 128");
     if (batch == 0 || nrhs == 0) return;
     const uint32_t N = n <= 4 ? 4 : n <= 8 ? 8 : n <= 16 ? 16 : n <= 32 ? 32 : 64;
     if (cdiv(nrhs, N) > kMaxGridY) invalid("[solve] too many right-hand sides for one call");
@@ -516,7 +577,7 @@ void lu_small_solve(const float* a, const float* b, uint32_t nrhs, float* x, uin
 }
 
 void lu_small_inv(const float* a, float* x, uint32_t* info, uint32_t batch, uint32_t n, hipStream_t s) {
-    if (!lu_small_fits(n)) invalid("[inv] lu_small takes n <= 64");
+    if (!lu_small_factor_fits(n)) invalid("[inv] lu_small takes n <= 128");
     if (batch == 0) return;
     dispatch_lu<kInv>(a, nullptr, nullptr, info, nullptr, x, batch, n, n, s, "lu_small_inv");
 }

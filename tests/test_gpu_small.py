@@ -163,7 +163,7 @@ def test_solve_shapes(cuda, api, oracle, n, nrhs):
             assert (np.abs(y - yo).max(axis=(-2, -1)) / np.abs(yo).max(axis=(-2, -1))).max() <= 1e-4
 
 
-@pytest.mark.parametrize("n", [1, 2, 5, 16, 32, 33, 64])
+@pytest.mark.parametrize("n", [1, 2, 5, 16, 32, 33, 64, 65, 128])
 def test_lu_inv_shapes(cuda, api, oracle, n):
     a = gaussian((60, n, n), seed=n + 100)
     lu, piv, info = api.lu_factor(a)
@@ -243,4 +243,25 @@ def test_solve_triangular_one_workgroup(cuda, api, oracle, n, nrhs, upper, unit)
     yo = oracle.solve_triangular(a, b, upper, unit)
     assert not np.isnan(y).any()
     assert (np.abs(y - yo).max(axis=(-2, -1)) / np.abs(yo).max(axis=(-2, -1))).max() <= 1e-4
+
+
+@pytest.mark.parametrize("n", [65, 100, 128])
+@pytest.mark.parametrize("nrhs", [1, 17, 70])
+def test_solve_one_workgroup(cuda, api, oracle, n, nrhs):
+    """65 <= n <= 128: factor, permutation and substitutions in one workgroup
+    per matrix (right-hand sides beyond 64 in a second workgroup); a matrix
+    with a zero column gives NaN there and LAPACK's info."""
+    a = gaussian((24, n, n), seed=n * 7 + nrhs) + np.float32(2 * n) * np.eye(n, dtype=np.float32)
+    a[3, :, n // 2] = 0.0
+    b = gaussian((24, n, nrhs), seed=nrhs)
+    x, info = api.solve(a, b)
+    xo, io = oracle.solve(a, b)
+    assert np.array_equal(u32(info), io) and u32(info)[3] == n // 2 + 1 and np.count_nonzero(u32(info)) == 1
+    assert np.isnan(x[3]).all()
+    ok = np.setdiff1d(np.arange(a.shape[0]), [3])
+    x, xo, a, b = x[ok], xo[ok], a[ok], b[ok]
+    r = np.linalg.norm(a.astype(np.float64) @ x - b, axis=(-2, -1)) / (
+        np.linalg.norm(a.astype(np.float64), axis=(-2, -1)) * np.linalg.norm(x.astype(np.float64), axis=(-2, -1)))
+    assert r.max() <= bound(n)
+    assert (np.abs(x - xo).max(axis=(-2, -1)) / np.abs(xo).max(axis=(-2, -1))).max() <= 1e-4
 
