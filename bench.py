@@ -163,6 +163,24 @@ def workloads():
         lambda api, t: api.solve(t["a"], t["b"]), "lu_small_solve", 8192 * (1024 + 256 + 256 + 4),
         8192 * (2731 + 2 * 16 * 16 * 4), "hbm",
         lambda o, h, n: o.solve(h["a"][:n], h["b"][:n]), {"batch": 8192, "n": 16, "nrhs": 4})
+    def mid_make(spd):
+        def make():
+            rng = np.random.default_rng(7 if spd else 8)
+            g = rng.standard_normal((4096, 128, 128), dtype=np.float32)
+            if spd:
+                g = (np.matmul(g, np.swapaxes(g, -1, -2)) + np.float32(128) * np.eye(128, dtype=np.float32))
+            return {"a": np.ascontiguousarray(g, dtype=np.float32)}
+        return make
+
+    # batched shapes beyond the configs: one matrix per workgroup in LDS
+    w["cholesky128"] = Workload(
+        "cholesky128", "cholesky lower, 4096 x 128x128 SPD fp32 (G G^T + 128 I)", 4096, mid_make(True),
+        lambda api, t: api.cholesky(t["a"], False), "chol_small", 4096 * (65536 + 65536 + 4), 4096 * 699051, "hbm",
+        lambda o, h, n: o.cholesky(h["a"][:n], False), {"batch": 4096, "n": 128})
+    w["lu128"] = Workload(
+        "lu128", "lu_factor, 4096 x 128x128 fp32 N(0,1)", 4096, mid_make(False),
+        lambda api, t: api.lu_factor(t["a"]), "lu_small_factor", 4096 * (65536 + 65536 + 512 + 4), 4096 * 1398101,
+        "hbm", lambda o, h, n: o.lu_factor(h["a"][:n]), {"batch": 4096, "n": 128})
     w["trsm"] = Workload(
         "trsm", "solve_triangular lower unit, 8192 x 16x16 fp32, 4 right-hand sides (BASELINE config 4)", 8192,
         lu_make, lambda api, t: api.solve_triangular(t["a"], t["b"], False, True), "trsm_small",
