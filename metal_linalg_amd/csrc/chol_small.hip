@@ -96,7 +96,7 @@ __global__ __launch_bounds__(64) void chol_small_kernel(const float* __restrict_
 // LDS (row stride n + 1, 66 KB at n = 128: two workgroups per CU),
 // right-looking with the same arithmetic as above: the pivot's square root,
 // the column times its reciprocal, the rank-1 update of the trailing lower
-// triangle.  The first pivot that is not positive and finite ends the loop
+// triangle; two workgroup barriers per column.  The first pivot that is not positive and finite ends the loop
 // in every thread at once (all read the same LDS word) and sets info.
 constexpr int kMidN = 128;
 
@@ -122,17 +122,15 @@ __global__ __launch_bounds__(256) void chol_mid_kernel(const float* __restrict__
         }
         const float lkk = sqrtf(d);
         const float inv = 1.0f / lkk;
-        __syncthreads();   // every thread has read the pivot
-        if (t == 0) a[k * ld + k] = lkk;
+        // the diagonal entry is written in the update phase, which reads no
+        // diagonal entry, so no thread can see it change before reading d
         for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] *= inv;
         __syncthreads();
-        const int m = nn - k - 1;
-        for (int idx = t; idx < m * m; idx += 256) {
-            const int i = idx / m, j = idx - i * m;
-            if (j <= i) {
-                const int r = k + 1 + i, c = k + 1 + j;
-                a[r * ld + c] = fmaf(-a[r * ld + k], a[c * ld + k], a[r * ld + c]);
-            }
+        if (t == 0) a[k * ld + k] = lkk;
+        // rows to the four waves in turn, columns to the lanes
+        for (int r = k + 1 + (t >> 6); r < nn; r += 4) {
+            const float lr = a[r * ld + k];
+            for (int c = k + 1 + (t & 63); c <= r; c += 64) a[r * ld + c] = fmaf(-lr, a[c * ld + k], a[r * ld + c]);
         }
         __syncthreads();
     }

@@ -381,6 +381,7 @@ __global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A
     __shared__ float a[kMidN * (kMidN + 1)];
     __shared__ float wb[4];
     __shared__ int wi[4];
+    __shared__ float wval[4];
     __shared__ int piv_sh[kMidN];
     __shared__ int perm[YR];
     __shared__ float ysh[YR][65];
@@ -410,39 +411,46 @@ __global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A
             const int oi = __shfl_xor(bi, off, 64);
             piv_take(b, bi, ob, oi, k);
         }
-        if (lane == 0) {
+        if (lane == 0) {   // each wave's candidate with its signed value, read before any write of this step
             wb[wv] = b;
             wi[wv] = bi;
+            wval[wv] = a[(bi < nn ? bi : k) * ld + k];
         }
         __syncthreads();
-        if (t == 0) {
-            for (int q = 1; q < 4; ++q) piv_take(b, bi, wb[q], wi[q], k);
-            piv_sh[k] = bi;
+        // every thread combines the four candidates in the same order
+        b = wb[0];
+        bi = wi[0];
+        float piv = wval[0];
+        for (int q = 1; q < 4; ++q) {
+            const int before = bi;
+            piv_take(b, bi, wb[q], wi[q], k);
+            if (bi != before) piv = wval[q];
         }
-        __syncthreads();
-        const int p = piv_sh[k];
+        const int p = bi;
+        if (t == 0) piv_sh[k] = p;
+        // rows k and p swapped in every column but k; column k is swapped and
+        // scaled by the threads that scale it, and its diagonal entry (the
+        // pivot) is written in the update phase, which reads no diagonal
         if (p != k)
-            for (int c = t; c < nn; c += 256) {
-                const float x = a[k * ld + c];
-                a[k * ld + c] = a[p * ld + c];
-                a[p * ld + c] = x;
-            }
-        __syncthreads();
-        const float piv = a[k * ld + k];
-        if (piv == 0.0f) {
-            if (info == 0) info = k + 1;
-        } else if (fabsf(piv) >= kSfmin) {
-            const float inv = 1.0f / piv;
-            for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] *= inv;
-        } else {
-            for (int r = k + 1 + t; r < nn; r += 256) a[r * ld + k] /= piv;
+            for (int c = t; c < nn; c += 256)
+                if (c != k) {
+                    const float x = a[k * ld + c];
+                    a[k * ld + c] = a[p * ld + c];
+                    a[p * ld + c] = x;
+                }
+        const bool big = fabsf(piv) >= kSfmin;
+        const float inv = 1.0f / piv;
+        for (int r = k + 1 + t; r < nn; r += 256) {
+            const float v = r == p ? a[k * ld + k] : a[r * ld + k];
+            a[r * ld + k] = piv == 0.0f ? v : (big ? v * inv : v / piv);
         }
+        if (piv == 0.0f && info == 0) info = k + 1;
         __syncthreads();
-        const int m = nn - k - 1;
-        for (int e = t; e < m * m; e += 256) {
-            const int i = e / m, j = e - i * m;
-            const int r = k + 1 + i, c = k + 1 + j;
-            a[r * ld + c] = fmaf(-a[r * ld + k], a[k * ld + c], a[r * ld + c]);
+        if (t == 0) a[k * ld + k] = piv;
+        // rows to the four waves in turn, columns to the lanes
+        for (int r = k + 1 + wv; r < nn; r += 4) {
+            const float lr = a[r * ld + k];
+            for (int c = k + 1 + lane; c < nn; c += 64) a[r * ld + c] = fmaf(-lr, a[k * ld + c], a[r * ld + c]);
         }
         __syncthreads();
     }
