@@ -12,6 +12,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -59,12 +60,37 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None) -> str:
+def _includes(path: str, seen: set) -> set:
+    """path and the in-tree headers it includes, transitively."""
+    if path in seen or not os.path.exists(path):
+        return seen
+    seen.add(path)
+    with open(path) as f:
+        for line in f:
+            m = re.match(r'\s*#\s*include\s*[<"]([^>"]+)[>"]', line)
+            if m:
+                for d in (CSRC, os.path.join(ROOT, "include")):
+                    _includes(os.path.join(d, m.group(1)), seen)
+    return seen
+
+
+def _stale(src: str) -> bool:
+    """The object is missing or older than its source or a header it includes."""
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    if not os.path.exists(obj):
+        return True
+    return os.path.getmtime(obj) < max(os.path.getmtime(d) for d in _includes(src, set()))
+
+
+def build(jobs: int | None = None, incremental: bool = False) -> str:
+    """Compile every source (or, with incremental, only the stale ones) and link."""
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
-    jobs = jobs or min(8, len(srcs), os.cpu_count() or 1)
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    jobs = jobs or max(1, min(8, len(todo), os.cpu_count() or 1))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        list(ex.map(_compile, todo))
+    objs = [os.path.join(BUILD, os.path.basename(s) + ".o") for s in srcs]
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs + ["-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -75,4 +101,4 @@ def build(jobs: int | None = None) -> str:
 
 
 if __name__ == "__main__":
-    print(build())
+    print(build(incremental="--incremental" in sys.argv))

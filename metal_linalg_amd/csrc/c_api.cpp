@@ -1,15 +1,24 @@
-// The C ABI (include/metal_linalg/c_api.h) over the buffer core: argument
-// checks, exceptions turned into status codes, the message kept per thread.
-// Behaviour follows the reference's src/c_api.cpp:17-401 (guarded(),
-// present(), the per-call checks and the policy get/set field copies).
+// The C ABI (include/metal_linalg/c_api.h) over the buffer core.
+//
+// Each decomposition entry point is one row of the same shape: the caller's
+// buffers listed with their element counts (a buffer may be NULL only when
+// it holds nothing), then the core call.  enter() applies the buffer rule in
+// the listed order; run_entry (entry.hpp) turns whatever the core throws
+// into a status code, keeping the message for metal_linalg_last_error() on
+// the calling thread.
+// Observable behaviour (statuses, messages, which check reports first)
+// follows the reference's src/c_api.cpp:17-190.
 #include <metal_linalg/c_api.h>
 
 #include <algorithm>
+#include <exception>
+#include <initializer_list>
 #include <new>
 #include <stdexcept>
 #include <string>
 
 #include "core.hpp"
+#include "entry.hpp"
 #include "policy.hpp"
 #include "runtime.hpp"
 
@@ -18,132 +27,105 @@ using mla::core::QrMode;
 
 namespace {
 
-thread_local std::string g_last_error;
+// A caller buffer as the buffer rule sees it.
+struct Buf {
+    const char* name;   // the argument's name in the message
+    const void* ptr;
+    uint64_t count;     // elements it holds for this call
+};
 
-template <class F>
-metal_linalg_status guarded(F&& f) {
-    try {
-        f();
-        return METAL_LINALG_OK;
-    } catch (const std::invalid_argument& e) {
-        g_last_error = e.what();
-        return METAL_LINALG_INVALID_ARGUMENT;
-    } catch (const std::bad_alloc&) {
-        g_last_error = "out of memory";
-        return METAL_LINALG_OUT_OF_MEMORY;
-    } catch (const std::exception& e) {
-        g_last_error = e.what();
-        return METAL_LINALG_RUNTIME_ERROR;
-    } catch (...) {
-        g_last_error = "unknown error";
-        return METAL_LINALG_RUNTIME_ERROR;
-    }
+template <class Work>
+metal_linalg_status enter(const char* op, std::initializer_list<Buf> bufs, Work&& work) noexcept {
+    return mla::run_entry([&] {
+        for (const Buf& b : bufs)
+            if (b.ptr == nullptr && b.count != 0)
+                throw std::invalid_argument(std::string("[") + op + "] " + b.name + " is NULL");
+        work();
+    });
 }
 
-void require(bool ok, const char* what) {
-    if (!ok) throw std::invalid_argument(what);
+metal_linalg_status reject(const char* message) noexcept {
+    mla::last_error_message() = message;
+    return METAL_LINALG_INVALID_ARGUMENT;
 }
 
-// A buffer may be NULL only when it holds nothing.
-bool present(const void* p, uint64_t count) { return p != nullptr || count == 0; }
+uint64_t elems(uint64_t batch, uint64_t rows, uint64_t cols) { return batch * rows * cols; }
 
 }  // namespace
 
 extern "C" {
 
-const char* metal_linalg_last_error(void) { return g_last_error.c_str(); }
+const char* metal_linalg_last_error(void) { return mla::last_error_message().c_str(); }
 
 metal_linalg_status metal_linalg_qr(const float* a, uint32_t batch, uint32_t rows, uint32_t cols, float* q,
                                     float* r) {
-    return guarded([&] {
-        const uint64_t k = std::min(rows, cols);
-        require(present(a, (uint64_t)batch * rows * cols), "[qr] a is NULL");
-        require(present(q, (uint64_t)batch * rows * k), "[qr] q is NULL");
-        require(present(r, (uint64_t)batch * k * cols), "[qr] r is NULL");
-        mla::core::qr({a, batch, rows, cols}, q, r, QrMode::reduced);
-    });
+    const uint64_t k = std::min(rows, cols);
+    return enter("qr", {{"a", a, elems(batch, rows, cols)}, {"q", q, elems(batch, rows, k)},
+                        {"r", r, elems(batch, k, cols)}},
+                 [&] { mla::core::qr({a, batch, rows, cols}, q, r, QrMode::reduced); });
 }
 
 metal_linalg_status metal_linalg_qr_with_mode(const float* a, uint32_t batch, uint32_t rows, uint32_t cols,
                                               metal_linalg_qr_mode mode, float* q, float* r) {
-    return guarded([&] {
-        require(mode == METAL_LINALG_QR_REDUCED || mode == METAL_LINALG_QR_R || mode == METAL_LINALG_QR_COMPLETE,
-                "[qr] mode must be METAL_LINALG_QR_REDUCED, _R or _COMPLETE");
-        const QrMode m = mode == METAL_LINALG_QR_R          ? QrMode::r
-                         : mode == METAL_LINALG_QR_COMPLETE ? QrMode::complete
-                                                            : QrMode::reduced;
-        const uint64_t qc = mla::core::qr_q_cols(m, rows, cols), rr = mla::core::qr_r_rows(m, rows, cols);
-        require(present(a, (uint64_t)batch * rows * cols), "[qr] a is NULL");
-        if (qc) require(present(q, (uint64_t)batch * rows * qc), "[qr] q is NULL");
-        require(present(r, (uint64_t)batch * rr * cols), "[qr] r is NULL");
-        mla::core::qr({a, batch, rows, cols}, qc ? q : nullptr, r, m);
-    });
+    QrMode m;
+    switch (mode) {
+        case METAL_LINALG_QR_REDUCED: m = QrMode::reduced; break;
+        case METAL_LINALG_QR_R: m = QrMode::r; break;
+        case METAL_LINALG_QR_COMPLETE: m = QrMode::complete; break;
+        default: return reject("[qr] mode must be METAL_LINALG_QR_REDUCED, _R or _COMPLETE");
+    }
+    const uint64_t qc = mla::core::qr_q_cols(m, rows, cols), rr = mla::core::qr_r_rows(m, rows, cols);
+    // q is not read when the mode forms no Q (its count is then zero)
+    return enter("qr", {{"a", a, elems(batch, rows, cols)}, {"q", q, elems(batch, rows, qc)},
+                        {"r", r, elems(batch, rr, cols)}},
+                 [&] { mla::core::qr({a, batch, rows, cols}, qc ? q : nullptr, r, m); });
 }
 
 metal_linalg_status metal_linalg_eigh(const float* a, uint32_t batch, uint32_t n, int lower, float* w, float* v,
                                       uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[eigh] a is NULL");
-        require(present(w, (uint64_t)batch * n), "[eigh] w is NULL");
-        mla::core::eigh({a, batch, n, n}, lower != 0, w, v, info);
-    });
+    return enter("eigh", {{"a", a, elems(batch, n, n)}, {"w", w, elems(batch, n, 1)}},
+                 [&] { mla::core::eigh({a, batch, n, n}, lower != 0, w, v, info); });
 }
 
 metal_linalg_status metal_linalg_svd(const float* a, uint32_t batch, uint32_t rows, uint32_t cols, float* u,
                                      float* s, float* vt, uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * rows * cols), "[svd] a is NULL");
-        require(present(s, (uint64_t)batch * std::min(rows, cols)), "[svd] s is NULL");
-        require((u == nullptr) == (vt == nullptr), "[svd] u and vt must both be given or both be NULL");
+    return enter("svd", {{"a", a, elems(batch, rows, cols)}, {"s", s, elems(batch, std::min(rows, cols), 1)}}, [&] {
+        if ((u == nullptr) != (vt == nullptr))
+            throw std::invalid_argument("[svd] u and vt must both be given or both be NULL");
         mla::core::svd({a, batch, rows, cols}, u, s, vt, info);
     });
 }
 
 metal_linalg_status metal_linalg_cholesky(const float* a, uint32_t batch, uint32_t n, int upper, float* l,
                                           uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[cholesky] a is NULL");
-        require(present(l, (uint64_t)batch * n * n), "[cholesky] l is NULL");
-        mla::core::cholesky({a, batch, n, n}, upper != 0, l, info);
-    });
+    return enter("cholesky", {{"a", a, elems(batch, n, n)}, {"l", l, elems(batch, n, n)}},
+                 [&] { mla::core::cholesky({a, batch, n, n}, upper != 0, l, info); });
 }
 
 metal_linalg_status metal_linalg_lu_factor(const float* a, uint32_t batch, uint32_t n, float* lu, uint32_t* pivots,
                                            uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[lu_factor] a is NULL");
-        require(present(lu, (uint64_t)batch * n * n), "[lu_factor] lu is NULL");
-        require(present(pivots, (uint64_t)batch * n), "[lu_factor] pivots is NULL");
-        mla::core::lu_factor({a, batch, n, n}, lu, pivots, info);
-    });
+    return enter("lu_factor",
+                 {{"a", a, elems(batch, n, n)}, {"lu", lu, elems(batch, n, n)}, {"pivots", pivots, elems(batch, n, 1)}},
+                 [&] { mla::core::lu_factor({a, batch, n, n}, lu, pivots, info); });
 }
 
 metal_linalg_status metal_linalg_solve(const float* a, uint32_t batch, uint32_t n, const float* b, uint32_t nrhs,
                                        float* x, uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[solve] a is NULL");
-        require(present(b, (uint64_t)batch * n * nrhs), "[solve] b is NULL");
-        require(present(x, (uint64_t)batch * n * nrhs), "[solve] x is NULL");
-        mla::core::solve({a, batch, n, n}, b, nrhs, x, info);
-    });
+    return enter("solve",
+                 {{"a", a, elems(batch, n, n)}, {"b", b, elems(batch, n, nrhs)}, {"x", x, elems(batch, n, nrhs)}},
+                 [&] { mla::core::solve({a, batch, n, n}, b, nrhs, x, info); });
 }
 
 metal_linalg_status metal_linalg_inv(const float* a, uint32_t batch, uint32_t n, float* x, uint32_t* info) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[inv] a is NULL");
-        require(present(x, (uint64_t)batch * n * n), "[inv] x is NULL");
-        mla::core::inv({a, batch, n, n}, x, info);
-    });
+    return enter("inv", {{"a", a, elems(batch, n, n)}, {"x", x, elems(batch, n, n)}},
+                 [&] { mla::core::inv({a, batch, n, n}, x, info); });
 }
 
 metal_linalg_status metal_linalg_solve_triangular(const float* a, uint32_t batch, uint32_t n, const float* b,
                                                   uint32_t nrhs, int upper, int unit, float* x) {
-    return guarded([&] {
-        require(present(a, (uint64_t)batch * n * n), "[solve_triangular] a is NULL");
-        require(present(b, (uint64_t)batch * n * nrhs), "[solve_triangular] b is NULL");
-        require(present(x, (uint64_t)batch * n * nrhs), "[solve_triangular] x is NULL");
-        mla::core::solve_triangular({a, batch, n, n}, b, nrhs, upper != 0, unit != 0, x);
-    });
+    return enter("solve_triangular",
+                 {{"a", a, elems(batch, n, n)}, {"b", b, elems(batch, n, nrhs)}, {"x", x, elems(batch, n, nrhs)}},
+                 [&] { mla::core::solve_triangular({a, batch, n, n}, b, nrhs, upper != 0, unit != 0, x); });
 }
 
 // ---- Metal buffers: no such thing on this platform ----

@@ -344,6 +344,15 @@ void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t*
     } else {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
         float* work = static_cast<float*>(call.scratch(lu_blocked_workspace(n)));
+        // the blocked path gathers b's rows into x: an x that overlaps b
+        // (a solve in place) reads a copy of b instead
+        const size_t bytes = (size_t)B * n * nrhs * sizeof(float);
+        const char *xb = reinterpret_cast<const char*>(dx), *bb = reinterpret_cast<const char*>(db);
+        if (xb < bb + bytes && bb < xb + bytes) {
+            float* copy = call.tmp<float>((size_t)B * n * nrhs);
+            MLA_HIP(hipMemcpyAsync(copy, db, bytes, hipMemcpyDeviceToDevice, call.stream()));
+            db = copy;
+        }
         lu_blocked_solve(da, db, nrhs, dx, di, work, B, n, call.stream());
     }
     call.finish();

@@ -368,25 +368,31 @@ __device__ __forceinline__ void piv_take(float& b, int& i, float ob, int oi, int
     }
 }
 
-// Solve and inverse (MODE != kFactor) go on in the same workgroup: the swaps
-// composed into one row permutation, 64 right-hand sides gathered through
-// it into LDS (blockIdx.y picks which 64), and the first wave substitutes,
-// one right-hand side per lane, in the order of the kernels above.
-template <int MODE>
-__global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A, float* __restrict__ LU,
+// Solve and inverse (MODE != kFactor) go on in the same workgroup, after
+// the one factorization: the swaps composed into one row permutation, then
+// the right-hand sides in passes of 4 * (64 / G) columns.  In a pass, each
+// wave takes 64 / G columns with G lanes per column; lane q of a column holds
+// rows q, q + G, q + 2G, ... in registers, so a substitution step is one
+// broadcast of y_k within the column's lanes and up to 128 / G multiply-adds
+// per lane, in the order of the kernels above.  Every read of A (into LDS)
+// and of the pass's right-hand sides comes before any write of the same
+// columns of X, so X may alias A (inv) or B (solve).
+template <int MODE, int G>
+__global__ __launch_bounds__(256) void lu_mid_kernel(const float* A, float* __restrict__ LU,
                                                      uint32_t* __restrict__ pivots, uint32_t* __restrict__ info_out,
-                                                     const float* __restrict__ B, float* __restrict__ X, uint32_t n,
-                                                     uint32_t nrhs) {
-    constexpr int YR = MODE == kFactor ? 1 : kMidN;
-    __shared__ float a[kMidN * (kMidN + 1)];
+                                                     const float* B, float* X, uint32_t n, uint32_t nrhs) {
+    // row stride kLda at every n: a row's offset is a compile-time constant
+    // in the unrolled substitutions (an immediate in the LDS instruction)
+    constexpr int kLda = kMidN + 1;
+    __shared__ float a[kMidN * kLda];
     __shared__ float wb[4];
     __shared__ int wi[4];
     __shared__ float wval[4];
     __shared__ int piv_sh[kMidN];
-    __shared__ int perm[YR];
-    __shared__ float ysh[YR][65];
+    __shared__ int perm[kMidN];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int nn = (int)n, ld = nn + 1;
+    const int nn = (int)n;
+    constexpr int ld = kLda;
     const size_t mat = blockIdx.x;
     const float* src = A + mat * (size_t)n * n;
     for (int e = t; e < nn * nn; e += 256) {
@@ -463,47 +469,75 @@ __global__ __launch_bounds__(256) void lu_mid_kernel(const float* __restrict__ A
             dst[e] = a[r * ld + c];
         }
     } else {
-        for (int r = t; r < nn; r += 256) perm[r] = r;
-        __syncthreads();
-        if (t == 0)
-            for (int k = 0; k < nn; ++k) {   // position r of P b is row perm[r] of b
+        constexpr int R = kMidN / G;        // rows per lane
+        constexpr int CPW = 64 / G;         // columns per wave
+        if (t == 0) {   // position r of P b is row perm[r] of b
+            for (int r = 0; r < nn; ++r) perm[r] = r;
+            for (int k = 0; k < nn; ++k) {
                 const int p = piv_sh[k];
                 const int x = perm[k];
                 perm[k] = perm[p];
                 perm[p] = x;
             }
+            if (info_out) info_out[mat] = (uint32_t)info;
+        }
         __syncthreads();
-        const int col0 = (int)blockIdx.y * 64;
+        const int q = lane % G;             // this lane's rows: q + G i
+        const int base = lane - q;          // the column's first lane
         const int nr = MODE == kInv ? nn : (int)nrhs;
         const float* bsrc = MODE == kInv ? nullptr : B + mat * (size_t)n * nr;
-        for (int e = t; e < nn * 64; e += 256) {
-            const int r = e >> 6, j = e & 63;
-            float v = 0.0f;
-            if (col0 + j < nr) {
-                const int sr = perm[r];
-                v = MODE == kInv ? (sr == col0 + j ? 1.0f : 0.0f) : bsrc[(size_t)sr * nr + col0 + j];
-            }
-            ysh[r][j] = v;
-        }
-        __syncthreads();
-        if (t < 64) {
-            const int j = t;
-            for (int k = 0; k < nn; ++k) {   // unit lower L
-                const float yk = ysh[k][j];
-                for (int r = k + 1; r < nn; ++r) ysh[r][j] = fmaf(-a[r * ld + k], yk, ysh[r][j]);
-            }
-            for (int k = nn - 1; k >= 0; --k) {   // U
-                const float v = ysh[k][j] / a[k * ld + k];
-                ysh[k][j] = v;
-                for (int r = 0; r < k; ++r) ysh[r][j] = fmaf(-a[r * ld + k], v, ysh[r][j]);
-            }
-        }
-        __syncthreads();
-        if (t == 0 && info_out && blockIdx.y == 0) info_out[mat] = (uint32_t)info;
         float* dst = X + mat * (size_t)n * nr;
-        for (int e = t; e < nn * 64; e += 256) {
-            const int r = e >> 6, j = e & 63;
-            if (col0 + j < nr) dst[(size_t)r * nr + col0 + j] = info ? qnan() : ysh[r][j];
+        for (int col0 = 0; col0 < nr; col0 += 4 * CPW) {
+            const int j = col0 + wv * CPW + lane / G;
+            const bool live = j < nr;
+            float y[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int r = G * i + q;
+                float v = 0.0f;
+                if (live && r < nn) {
+                    const int sr = perm[r];
+                    v = MODE == kInv ? (sr == j ? 1.0f : 0.0f) : bsrc[(size_t)sr * nr + j];
+                }
+                y[i] = v;
+            }
+            // unit lower L: y_r -= L(r, k) y_k for r > k
+            // (rows at or past n take part and are never read: no bound per row)
+#pragma clang loop unroll(full)
+            for (int kk = 0; kk < R; ++kk) {
+#pragma clang loop unroll(full)
+                for (int s = 0; s < G; ++s) {
+                    const int k = G * kk + s;
+                    if (k < nn) {
+                        const float yk = __shfl(y[kk], base + s, 64);
+                        if (q > s) y[kk] = fmaf(-a[(G * kk + q) * ld + k], yk, y[kk]);
+#pragma clang loop unroll(full)
+                        for (int i = kk + 1; i < R; ++i) y[i] = fmaf(-a[(G * i + q) * ld + k], yk, y[i]);
+                    }
+                }
+            }
+            // U: y_k /= U(k, k), then y_r -= U(r, k) y_k for r < k
+#pragma clang loop unroll(full)
+            for (int kk = R - 1; kk >= 0; --kk) {
+#pragma clang loop unroll(full)
+                for (int s = G - 1; s >= 0; --s) {
+                    const int k = G * kk + s;
+                    if (k < nn) {
+                        const float yk = __shfl(y[kk], base + s, 64) / a[k * ld + k];
+                        if (q == s) y[kk] = yk;
+                        if (q < s) y[kk] = fmaf(-a[(G * kk + q) * ld + k], yk, y[kk]);
+#pragma clang loop unroll(full)
+                        for (int i = 0; i < kk; ++i) y[i] = fmaf(-a[(G * i + q) * ld + k], yk, y[i]);
+                    }
+                }
+            }
+            if (live) {
+#pragma unroll
+                for (int i = 0; i < R; ++i) {
+                    const int r = G * i + q;
+                    if (r < nn) dst[(size_t)r * nr + j] = info ? qnan() : y[i];
+                }
+            }
         }
     }
 }
@@ -534,10 +568,18 @@ void dispatch_lu(const float* a, float* lu, uint32_t* piv, uint32_t* info, const
         hipLaunchKernelGGL((lu_wide_kernel<MODE>), dim3(batch, chunks), dim3(64), 0, s, a, info, b, x, n, nrhs);
         t.stop();
     } else {
-        const uint32_t chunks = (uint32_t)cdiv(MODE == kSolve ? nrhs : n, 64);
+        // lanes per right-hand side: fewer columns, more lanes on each
+        const uint32_t nr = MODE == kSolve ? nrhs : n;
         KernelTimer t(name, s);
-        hipLaunchKernelGGL((lu_mid_kernel<MODE>), dim3(batch, chunks), dim3(256), 0, s, a, nullptr, nullptr, info, b,
-                           x, n, nrhs);
+        if (nr <= 16)
+            hipLaunchKernelGGL((lu_mid_kernel<MODE, 16>), dim3(batch), dim3(256), 0, s, a, nullptr, nullptr, info, b,
+                               x, n, nrhs);
+        else if (nr <= 32)
+            hipLaunchKernelGGL((lu_mid_kernel<MODE, 8>), dim3(batch), dim3(256), 0, s, a, nullptr, nullptr, info, b,
+                               x, n, nrhs);
+        else
+            hipLaunchKernelGGL((lu_mid_kernel<MODE, 4>), dim3(batch), dim3(256), 0, s, a, nullptr, nullptr, info, b,
+                               x, n, nrhs);
         t.stop();
     }
     MLA_HIP(hipGetLastError());
@@ -566,7 +608,7 @@ void lu_small_factor(const float* a, float* lu, uint32_t* pivots, uint32_t* info
     if (batch == 0) return;
     if (n > 64) {
         KernelTimer t("lu_small_factor", s);
-        hipLaunchKernelGGL(lu_mid_kernel<kFactor>, dim3(batch), dim3(256), 0, s, a, lu, pivots, info, nullptr,
+        hipLaunchKernelGGL((lu_mid_kernel<kFactor, 4>), dim3(batch), dim3(256), 0, s, a, lu, pivots, info, nullptr,
                            nullptr, n, 0u);
         t.stop();
         MLA_HIP(hipGetLastError());

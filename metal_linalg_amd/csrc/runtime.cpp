@@ -1,6 +1,8 @@
 // Runtime implementation: device, per-call staging, workspace, kernel timing.
 #include "runtime.hpp"
 
+#include "entry.hpp"
+
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -98,7 +100,9 @@ hipEvent_t get_event() {
     return e;
 }
 
-bool is_device_pointer(const void* p) {
+}  // namespace
+
+bool is_device_memory(const void* p) {
     if (!p) return false;
     hipPointerAttribute_t attr;
     std::memset(&attr, 0, sizeof(attr));
@@ -111,7 +115,28 @@ bool is_device_pointer(const void* p) {
            attr.type == hipMemoryTypeUnified;
 }
 
-}  // namespace
+std::string& last_error_message() {
+    thread_local std::string message;
+    return message;
+}
+
+metal_linalg_status status_of_current_exception() noexcept {
+    try {
+        throw;
+    } catch (const std::invalid_argument& e) {
+        last_error_message() = e.what();
+        return METAL_LINALG_INVALID_ARGUMENT;
+    } catch (const std::bad_alloc&) {
+        last_error_message() = "out of memory";
+        return METAL_LINALG_OUT_OF_MEMORY;
+    } catch (const std::exception& e) {
+        last_error_message() = e.what();
+        return METAL_LINALG_RUNTIME_ERROR;
+    } catch (...) {
+        last_error_message() = "unknown error";
+        return METAL_LINALG_RUNTIME_ERROR;
+    }
+}
 
 bool have_device() { return state().ok; }
 
@@ -189,7 +214,7 @@ void* Call::take(size_t bytes) {
 
 const void* Call::input(const void* p, size_t bytes) {
     if (bytes == 0) return p;
-    if (is_device_pointer(p)) return p;
+    if (is_device_memory(p)) return p;
     void* d = take(bytes);
     MLA_HIP(hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, dev_.stream));
     return d;
@@ -198,7 +223,7 @@ const void* Call::input(const void* p, size_t bytes) {
 void* Call::output(void* p, size_t bytes) {
     if (!p) return nullptr;
     if (bytes == 0) return p;
-    if (is_device_pointer(p)) return p;
+    if (is_device_memory(p)) return p;
     void* d = take(bytes);
     back_.push_back({p, d, bytes});
     return d;

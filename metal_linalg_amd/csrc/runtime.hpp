@@ -94,6 +94,9 @@ private:
 bool timing_enabled();
 void timing_collect();   // after a stream synchronisation
 
+// True for HIP device (or managed) memory; false for host memory and NULL.
+bool is_device_memory(const void* p);
+
 // ceil(a / b)
 inline uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 

@@ -22,16 +22,18 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 BUILD_DIR = os.path.join(HERE, "_build")
 LIB_PATH = os.path.join(BUILD_DIR, "liboracle.so")
-SOURCE = os.path.join(HERE, "lapack_batch.cpp")
+SOURCES = [os.path.join(HERE, "lapack_batch.cpp"), os.path.join(HERE, "lu_netlib.cpp")]
 
 
 def build(force: bool = True) -> str:
-    """Compile lapack_batch.cpp with g++ into oracle/_build/liboracle.so."""
+    """Compile lapack_batch.cpp and lu_netlib.cpp with g++ into
+    oracle/_build/liboracle.so (no FMA contraction: LAPACK's Fortran order)."""
     if not force and os.path.exists(LIB_PATH):
         return LIB_PATH
     os.makedirs(BUILD_DIR, exist_ok=True)
     tmp = LIB_PATH + ".tmp"
-    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-pthread", SOURCE, "-o", tmp, "-ldl"]
+    cmd = ["g++", "-O2", "-std=c++17", "-ffp-contract=off", "-shared", "-fPIC", "-pthread", *SOURCES, "-o", tmp,
+           "-ldl"]
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
@@ -76,6 +78,9 @@ def lib():
     L.oracle_solve.argtypes = [_p, _u32, _u32, _p, _u32, _p, _p]
     L.oracle_inv.argtypes = [_p, _u32, _u32, _p, _p]
     L.oracle_solve_triangular.argtypes = [_p, _u32, _u32, _p, _u32, ctypes.c_int, ctypes.c_int, _p]
+    L.oracle_lu_netlib_factor.argtypes = [_p, _u32, _u32, _p, _p, _p]
+    L.oracle_lu_netlib_solve.argtypes = [_p, _u32, _u32, _p, _u32, _p, _p]
+    L.oracle_lu_netlib_inv.argtypes = [_p, _u32, _u32, _p, _p]
     if L.oracle_init(lapack_path().encode()) != 0:
         raise RuntimeError(L.oracle_last_error().decode())
     _lib = L
@@ -199,3 +204,34 @@ def solve_triangular(a, rhs, upper: bool = False, unit: bool = False):
     x = np.empty_like(rhs)
     _check(lib().oracle_solve_triangular(_ptr(a), b, n, _ptr(rhs), nrhs, int(bool(upper)), int(bool(unit)), _ptr(x)))
     return x
+
+
+# ---- netlib LAPACK restatement (lu_netlib.cpp): the pin for non-finite LU inputs ----
+
+def lu_netlib_factor(a):
+    """(LU, pivots, info) by netlib's sgetf2 rule (ISAMAX: strict '>', NaN never taken)."""
+    a = _c(a)
+    lead, b, n, _ = _shape3(a)
+    lu = np.empty_like(a)
+    piv = np.empty(lead + (n,), np.uint32)
+    info = np.empty(lead, np.uint32)
+    lib().oracle_lu_netlib_factor(_ptr(a), b, n, _ptr(lu), _ptr(piv), _ptr(info))
+    return lu, piv, info
+
+
+def lu_netlib_solve(a, rhs):
+    a, rhs = _c(a), _c(rhs)
+    lead, b, n, _ = _shape3(a)
+    x = np.empty_like(rhs)
+    info = np.empty(lead, np.uint32)
+    lib().oracle_lu_netlib_solve(_ptr(a), b, n, _ptr(rhs), rhs.shape[-1], _ptr(x), _ptr(info))
+    return x, info
+
+
+def lu_netlib_inv(a):
+    a = _c(a)
+    lead, b, n, _ = _shape3(a)
+    x = np.empty_like(a)
+    info = np.empty(lead, np.uint32)
+    lib().oracle_lu_netlib_inv(_ptr(a), b, n, _ptr(x), _ptr(info))
+    return x, info

@@ -179,3 +179,27 @@ def config5_spd(g):
     n = g.shape[0]
     g64 = g.astype(np.float64)
     return (g64 @ g64.T / n + np.eye(n)).astype(np.float32)
+
+
+def near_tie(a, piv_x, piv_y, rel=1e-4):
+    """True when the first step at which two partial-pivoting sequences part
+    is a near-tie of column magnitudes: elimination in float64 along piv_y
+    up to that step, then |a[piv_x[k], k]| and |a[piv_y[k], k]| within rel
+    of each other (a NaN or an infinity never ties)."""
+    a = a.astype(np.float64).copy()
+    with np.errstate(all="ignore"):
+        for k in range(a.shape[0]):
+            if piv_x[k] != piv_y[k]:
+                m1, m2 = abs(a[piv_x[k], k]), abs(a[piv_y[k], k])
+                return bool(np.isfinite(m1) and np.isfinite(m2) and abs(m1 - m2) <= rel * max(m1, m2))
+            p = piv_y[k]
+            a[[k, p]] = a[[p, k]]
+            if a[k, k] != 0:
+                a[k + 1:, k] /= a[k, k]
+            a[k + 1:, k + 1:] -= np.outer(a[k + 1:, k], a[k, k + 1:])
+    return True
+
+
+def first_difference(piv_x, piv_y):
+    d = np.nonzero(np.asarray(piv_x) != np.asarray(piv_y))[0]
+    return int(d[0]) if d.size else -1

@@ -49,7 +49,7 @@ def test_reference_symbol_set_is_declared():
 def test_struct_layouts(lib):
     # field counts as the reference's c_api.h
     for what, count in {"qr": 12, "eigh": 30, "svd": 35, "cholesky": 10, "lu": 4, "trsm": 4}.items():
-        S = lib.POLICIES[what][0]
+        S = lib.policy_struct(what)
         assert ctypes.sizeof(S) == 4 * count
 
 

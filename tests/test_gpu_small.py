@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 import _kat
-from _util import bound, config4_lu, config4_spd, gaussian, lu_residual, rel_recon, to_np, u32
+from _util import (bound, config4_lu, config4_spd, first_difference, gaussian, lu_residual, near_tie, rel_recon,
+                   to_np, u32)
 
 pytestmark = pytest.mark.gpu
 
@@ -80,22 +81,6 @@ def test_cholesky_info_minors(cuda, api, oracle, n):
     assert u32(info)[0] == oracle.cholesky(x, False)[1][0] == 10
 
 
-def near_tie(a, piv_gpu, piv_ref, rel=1e-4):
-    """First differing pivot step is a near-tie of |column| magnitudes."""
-    a = a.astype(np.float64).copy()
-    n = a.shape[0]
-    for k in range(n):
-        if piv_gpu[k] != piv_ref[k]:
-            m1, m2 = abs(a[piv_gpu[k], k]), abs(a[piv_ref[k], k])
-            return abs(m1 - m2) <= rel * max(m1, m2)
-        p = piv_ref[k]
-        a[[k, p]] = a[[p, k]]
-        if a[k, k] != 0:
-            a[k + 1:, k] /= a[k, k]
-            a[k + 1:, k + 1:] -= np.outer(a[k + 1:, k], a[k, k + 1:])
-    return True
-
-
 def test_config4_lu_solve_trsm(cuda, api, oracle):
     torch = cuda
     a, b = config4_lu()
@@ -107,11 +92,13 @@ def test_config4_lu_solve_trsm(cuda, api, oracle):
     res = lu_residual(a, lu, piv)
     print(f"[lu config4] PA-LU max {res.max():.3e} bound {bound(16):.3e}")
     assert res.max() <= bound(16)
+    # pivots are index outputs: identical to LAPACK's, except where a
+    # difference is proven to start at a near-tie (each one printed)
     differ = np.nonzero(np.any(piv != pivo, axis=-1))[0]
     print(f"[lu config4] pivot sequences differing from LAPACK's: {len(differ)} of {a.shape[0]}")
-    assert len(differ) <= a.shape[0] // 1000
     for i in differ:
-        assert near_tie(a[i], piv[i], pivo[i]), i
+        print(f"[lu config4]   matrix {i}: first difference at step {first_difference(piv[i], pivo[i])}")
+        assert near_tie(a[i], piv[i], pivo[i], rel=1e-5), i
     same = np.setdiff1d(np.arange(a.shape[0]), differ)
     d = np.abs(lu[same] - luo[same]).max(axis=(-2, -1)) / np.abs(luo[same]).max(axis=(-2, -1))
     assert d.max() <= 1e-4
@@ -216,8 +203,10 @@ def test_lu_factor_one_matrix_per_wave(cuda, api, oracle, n):
     res = lu_residual(a, lu, piv)
     assert res.max() <= bound(n), res.max()
     differ = np.nonzero(np.any(piv != po, axis=-1))[0]
+    print(f"[lu n={n}] pivot sequences differing from LAPACK's: {len(differ)} of {a.shape[0]}")
     for i in differ:
-        assert near_tie(a[i], piv[i], po[i]), i
+        print(f"[lu n={n}]   matrix {i}: first difference at step {first_difference(piv[i], po[i])}")
+        assert near_tie(a[i], piv[i], po[i], rel=1e-5), i
     same = np.setdiff1d(np.arange(a.shape[0]), differ)
     d = np.abs(lu[same] - lo[same]).max(axis=(-2, -1)) / np.abs(lo[same]).max(axis=(-2, -1))
     assert d.max() <= 1e-3
