@@ -274,8 +274,10 @@ __device__ __forceinline__ void eigh_vectors(EighLds<N>& s, float (&x)[N], float
     // one's fall into its close group below.
     const float tol = fmaxf(kEps * tnorm, kSafeMin);   // smaller pivots become +-tol
     float u[N];
+    // the same start for every matrix: a matrix's result does not depend on
+    // where it sits in the batch
 #pragma unroll
-    for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)(mat * 64 + c), (uint32_t)k) : 0.0f;
+    for (int k = 0; k < N; ++k) x[k] = k < nn ? hash_uniform((uint32_t)c, (uint32_t)k) : 0.0f;
     // close eigenvalues: lanes cs .. c with gaps <= kOrtol |T|
     const float prev = __shfl_up(lam, 1, N);
     const bool brk = c == 0 || !mine || diag || lam - prev > kOrtol * tnorm;

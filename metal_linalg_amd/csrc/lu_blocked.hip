@@ -188,8 +188,9 @@ __device__ __forceinline__ void leaf_column(float (&a)[RPT][W], LeafShared& S, i
     }
     if (pv == 0.0f && zero_at == 0) zero_at = K + 1;
     if (t == 0) S.plist[K] = p;
-    // multipliers (rows below K) and the rank-1 update; rows <= K keep their
-    // values: multiplier 0
+    // multipliers (rows below K) and the rank-1 update of the rows below K
+    // only (rows <= K are not touched, as sger's: no 0 * NaN from a
+    // non-finite pivot row)
     if (pv != 0.0f) {   // uniform
         if (fabsf(pv) >= kSfmin) {
             const float inv = 1.0f / pv;
@@ -204,9 +205,11 @@ __device__ __forceinline__ void leaf_column(float (&a)[RPT][W], LeafShared& S, i
     }
 #pragma unroll
     for (int q = 0; q < RPT; ++q) {
-        const float l = (q >= G || R::row(t, q) > K) ? a[q][K] : 0.0f;
+        if (q >= G || R::row(t, q) > K) {   // rows past group 0 are all below K
+            const float l = a[q][K];
 #pragma unroll
-        for (int c = K + 1; c < W; ++c) a[q][c] = fmaf(-l, u[c], a[q][c]);
+            for (int c = K + 1; c < W; ++c) a[q][c] = fmaf(-l, u[c], a[q][c]);
+        }
     }
 }
 
