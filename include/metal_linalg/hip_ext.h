@@ -9,6 +9,8 @@
 
 #include <stdint.h>
 
+#include "c_api.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -46,6 +48,21 @@ int metal_linalg_hip_sytrd(const float* a, uint32_t n, int lower, float* d, floa
 
 /* The device's gcnArchName ("" without a GPU). */
 const char* metal_linalg_hip_arch(void);
+
+/* metal_linalg_eigh for n <= 64 that allocates nothing.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory while
+ * they run (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, results and info words as
+ * metal_linalg_eigh, but every non-NULL pointer must be HIP device memory
+ * (nothing is staged), and n must be at most 64 (else
+ * METAL_LINALG_INVALID_ARGUMENT).  The batched kernel's workspace (and info
+ * when `info` is NULL) lives in a fixed 8 MiB device array per GPU, found
+ * once per device; a batch larger than it serves (5405 matrices at n = 64
+ * with vectors) runs in chunks.  The array keeps the last call's contents
+ * and is shared by every call on the GPU: calls that overlapped on one GPU
+ * would race (the library serialises its own calls). */
+metal_linalg_status metal_linalg_hip_eigh_noalloc(const float* a, uint32_t batch, uint32_t n, int lower,
+                                                  float* w, float* v, uint32_t* info);
 
 #ifdef __cplusplus
 } /* extern "C" */
