@@ -32,9 +32,16 @@
 // LAPACK drivers whole, which run the same steps inside.
 
 #include <dlfcn.h>
+#include <link.h>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <memory>
 #include <cfloat>
 #include <cmath>
 #include <cstdint>
@@ -117,6 +124,14 @@ void scan_matrices(const float* a, uint32_t batch, uint32_t rows, uint32_t cols,
 }
 
 // ---- the reference's batch loop (metal_runtime.mm:402-432) ----
+//
+// A persistent pool of workers, one per host thread; a call cuts the batch
+// into 4 chunks per worker (kChunksPerThread) taken in turn.  Each worker
+// calls its own copy of the LAPACK library, loaded into a separate link
+// namespace (dlmopen): OpenBLAS serialises concurrent small calls from
+// different threads on its buffer-pool lock, which flattened the batch loop
+// at about 4 threads when every worker shared one copy.  Worker 0 uses the
+// copy oracle_init loaded; a copy that cannot be loaded falls back to it.
 uint32_t g_threads = 0;   // 0: every hardware thread
 
 uint32_t thread_count() {
@@ -125,12 +140,129 @@ uint32_t thread_count() {
     return h ? h : 1;
 }
 
+std::string g_path;                              // the library oracle_init loaded
+bool resolve_all(void* h, Lapack& L, const std::string& path);   // below
+// Copies are loaded into their own link namespaces (dlmopen; each brings its
+// own C runtime, so they share nothing), which glibc limits to 16 and static
+// TLS space to about 10: 8 copies, two workers sharing one at 16 threads
+// (measured: one copy per two workers scales as well as one per worker).
+constexpr uint32_t kMaxCopies = 8;
+std::vector<std::unique_ptr<Lapack>> g_copies;   // one per worker
+thread_local const Lapack* tls_lapack = nullptr;
+
+// The LAPACK of the calling thread (inside a batch: its worker's copy).
+const Lapack& lap();
+
+const Lapack* load_copy() {
+    const char* old = std::getenv("OPENBLAS_NUM_THREADS");
+    const std::string keep = old ? old : "";
+    setenv("OPENBLAS_NUM_THREADS", "1", 1);
+    void* h = dlmopen(LM_ID_NEWLM, g_path.c_str(), RTLD_NOW | RTLD_LOCAL);
+    if (old) setenv("OPENBLAS_NUM_THREADS", keep.c_str(), 1);
+    else unsetenv("OPENBLAS_NUM_THREADS");
+    if (!h) return nullptr;
+    auto L = std::make_unique<Lapack>();
+    if (!resolve_all(h, *L, g_path)) return nullptr;
+    if (L->set_num_threads) L->set_num_threads(1);
+    g_copies.push_back(std::move(L));
+    return g_copies.back().get();
+}
+
+class Pool {
+public:
+    // Runs job(b0, b1) over `chunks` contiguous pieces of [0, batch) on
+    // `workers` workers; rethrows the first exception.
+    void run(uint32_t workers, uint32_t batch, uint32_t chunks, const std::function<void(uint32_t, uint32_t)>& job) {
+        grow(workers);
+        std::unique_lock<std::mutex> lock(m_);
+        job_ = &job;
+        batch_ = batch;
+        chunks_ = chunks;
+        next_ = 0;
+        active_ = workers;
+        pending_ = workers;
+        error_ = nullptr;
+        ++generation_;
+        wake_.notify_all();
+        done_.wait(lock, [&] { return pending_ == 0; });
+        job_ = nullptr;
+        if (error_) std::rethrow_exception(error_);
+    }
+    ~Pool() {
+        {
+            std::lock_guard<std::mutex> lock(m_);
+            stop_ = true;
+            ++generation_;
+        }
+        wake_.notify_all();
+        for (auto& t : threads_) t.join();
+    }
+
+private:
+    void grow(uint32_t workers) {
+        while (threads_.size() < workers) {
+            const uint32_t w = (uint32_t)threads_.size();
+            const Lapack* L = &g_lapack;
+            const uint32_t slot = w % kMaxCopies;
+            while (g_copies.size() <= slot && load_copy()) {}
+            if (g_copies.size() > slot) L = g_copies[slot].get();
+            threads_.emplace_back([this, w, L] { loop(w, L); });
+        }
+    }
+    void loop(uint32_t w, const Lapack* L) {
+        tls_lapack = L;
+        uint64_t seen = 0;
+        for (;;) {
+            std::unique_lock<std::mutex> lock(m_);
+            wake_.wait(lock, [&] { return generation_ != seen; });
+            seen = generation_;
+            if (stop_) return;
+            if (w >= active_) continue;
+            const auto* job = job_;
+            lock.unlock();
+            for (uint32_t c; !failed_ && (c = next_.fetch_add(1)) < chunks_;) {
+                const uint32_t b0 = (uint32_t)((uint64_t)batch_ * c / chunks_);
+                const uint32_t b1 = (uint32_t)((uint64_t)batch_ * (c + 1) / chunks_);
+                try {
+                    (*job)(b0, b1);
+                } catch (...) {
+                    std::lock_guard<std::mutex> g(m_);
+                    if (!error_) error_ = std::current_exception();
+                    failed_ = true;
+                }
+            }
+            lock.lock();
+            if (--pending_ == 0) {
+                failed_ = false;
+                done_.notify_all();
+            }
+        }
+    }
+    std::mutex m_;
+    std::condition_variable wake_, done_;
+    std::vector<std::thread> threads_;
+    const std::function<void(uint32_t, uint32_t)>* job_ = nullptr;
+    uint32_t batch_ = 0, chunks_ = 0, active_ = 0, pending_ = 0;
+    std::atomic<uint32_t> next_{0};
+    std::atomic<bool> failed_{false};
+    std::exception_ptr error_;
+    uint64_t generation_ = 0;
+    bool stop_ = false;
+};
+
+Pool& pool() {
+    static Pool* p = new Pool();   // never destroyed: workers outlive static teardown order
+    return *p;
+}
+
+const Lapack& lap() { return tls_lapack ? *tls_lapack : g_lapack; }
+
 template <class F>
 void lapack_batches(uint32_t batch, const F& f) {
     const uint32_t threads = std::min<uint32_t>(thread_count(), batch);
-    if (threads <= 1) {
-        // one matrix (or one thread): LAPACK's own threads, as the reference
-        // leaves Accelerate threaded there (metal_runtime.mm:413-416)
+    if (batch <= 1) {
+        // one matrix: LAPACK's own threads, as the reference leaves
+        // Accelerate threaded there (metal_runtime.mm:413-416)
         if (g_lapack.set_num_threads) g_lapack.set_num_threads((int)thread_count());
         try {
             f(0u, batch);
@@ -142,29 +274,7 @@ void lapack_batches(uint32_t batch, const F& f) {
         return;
     }
     const uint32_t chunks = std::min<uint32_t>(batch, threads * 4);   // kChunksPerThread
-    std::atomic<uint32_t> next{0};
-    std::atomic<bool> failed{false};
-    std::mutex m;
-    std::exception_ptr error;
-    std::vector<std::thread> pool;
-    pool.reserve(threads);
-    for (uint32_t t = 0; t < threads; ++t) {
-        pool.emplace_back([&] {
-            for (uint32_t c; !failed && (c = next.fetch_add(1)) < chunks;) {
-                const uint32_t b0 = (uint32_t)((uint64_t)batch * c / chunks);
-                const uint32_t b1 = (uint32_t)((uint64_t)batch * (c + 1) / chunks);
-                try {
-                    f(b0, b1);
-                } catch (...) {
-                    std::lock_guard<std::mutex> lock(m);
-                    if (!error) error = std::current_exception();
-                    failed = true;
-                }
-            }
-        });
-    }
-    for (auto& t : pool) t.join();
-    if (error) std::rethrow_exception(error);
+    pool().run(threads, batch, chunks, std::function<void(uint32_t, uint32_t)>(f));
 }
 
 void transpose(const float* in, size_t ldi, float* out, size_t ldo, uint32_t rows, uint32_t cols) {
@@ -196,6 +306,25 @@ int guarded(F&& f) {
 
 constexpr float kNaN = std::numeric_limits<float>::quiet_NaN();
 
+bool resolve_all(void* h, Lapack& L, const std::string& path) {
+    const char* prefixes[] = {"scipy_", ""};
+    for (const char* p : prefixes) {
+        const bool ok = resolve(h, p, "sgeqrf_", L.sgeqrf) && resolve(h, p, "sorgqr_", L.sorgqr) &&
+                        resolve(h, p, "ssyevd_", L.ssyevd) && resolve(h, p, "sgesdd_", L.sgesdd) &&
+                        resolve(h, p, "spotrf_", L.spotrf) && resolve(h, p, "sgetrf_", L.sgetrf) &&
+                        resolve(h, p, "sgetrs_", L.sgetrs) && resolve(h, p, "sgetri_", L.sgetri) &&
+                        resolve(h, p, "cblas_sgemm", L.cblas_sgemm) && resolve(h, p, "cblas_strsm", L.cblas_strsm);
+        if (ok) {
+            resolve(h, p, "ssyevd_2stage_", L.ssyevd_2stage);
+            if (!resolve(h, p, "openblas_set_num_threads", L.set_num_threads)) L.set_num_threads = nullptr;
+            if (!resolve(h, p, "openblas_get_config", L.get_config)) L.get_config = nullptr;
+            L.name = path + " (prefix '" + p + "')";
+            return true;
+        }
+    }
+    return false;
+}
+
 }  // namespace
 
 extern "C" {
@@ -213,28 +342,13 @@ int oracle_init(const char* path) {
         return 2;
     }
     Lapack L{};
-    const char* prefixes[] = {"scipy_", ""};
-    bool ok = false;
-    for (const char* p : prefixes) {
-        ok = resolve(h, p, "sgeqrf_", L.sgeqrf) && resolve(h, p, "sorgqr_", L.sorgqr) &&
-             resolve(h, p, "ssyevd_", L.ssyevd) && resolve(h, p, "sgesdd_", L.sgesdd) &&
-             resolve(h, p, "spotrf_", L.spotrf) && resolve(h, p, "sgetrf_", L.sgetrf) &&
-             resolve(h, p, "sgetrs_", L.sgetrs) && resolve(h, p, "sgetri_", L.sgetri) &&
-             resolve(h, p, "cblas_sgemm", L.cblas_sgemm) && resolve(h, p, "cblas_strsm", L.cblas_strsm);
-        if (ok) {
-            resolve(h, p, "ssyevd_2stage_", L.ssyevd_2stage);
-            if (!resolve(h, p, "openblas_set_num_threads", L.set_num_threads)) L.set_num_threads = nullptr;
-            if (!resolve(h, p, "openblas_get_config", L.get_config)) L.get_config = nullptr;
-            L.name = std::string(path) + " (prefix '" + p + "')";
-            break;
-        }
-    }
-    if (!ok) {
+    if (!resolve_all(h, L, path)) {
         g_error = "oracle: the library lacks the LAPACK routines needed";
         return 2;
     }
     if (L.set_num_threads) L.set_num_threads(1);
     g_lapack = L;
+    g_path = path;
     g_ready = true;
     return 0;
 }
@@ -248,6 +362,10 @@ const char* oracle_lapack_config(void) {
 
 void oracle_set_threads(uint32_t n) { g_threads = n; }
 uint32_t oracle_threads(void) { return thread_count(); }
+
+// Copies of the LAPACK library loaded for the workers (0 until a batch has
+// run on more than one thread).
+uint32_t oracle_lapack_copies(void) { return (uint32_t)g_copies.size(); }
 
 // mode: 0 reduced, 1 R alone, 2 complete.  src/qr_cpu.mm:32-121
 int oracle_qr(const float* a, uint32_t batch, uint32_t M, uint32_t N, int mode, float* q_out, float* r_out) {
@@ -279,6 +397,7 @@ int oracle_qr(const float* a, uint32_t batch, uint32_t M, uint32_t N, int mode, 
         scan_matrices(a, batch, M, N, Part::all, amax.data(), finite.data());
 
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             lint lw = lwork, err = 0;
             std::vector<float> wa((size_t)M * wcols), tau(K), work(lwork);
             for (uint32_t b = b0; b < b1; ++b) {
@@ -328,12 +447,13 @@ int oracle_eigh(const float* a, uint32_t batch, uint32_t n, int lower, float* w_
         const bool two_stage = !v_out && n >= 128 && L.ssyevd_2stage != nullptr;
         const bool transpose_in = two_stage && lower;
         if (two_stage) uplo = 'L';
-        auto syevd = two_stage ? L.ssyevd_2stage : L.ssyevd;
         const size_t per = (size_t)n * n;
         std::vector<float> amax(batch);
         std::vector<char> finite(batch);
         scan_matrices(a, batch, n, n, lower ? Part::lower : Part::upper, amax.data(), finite.data());
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
+            auto syevd = two_stage ? L.ssyevd_2stage : L.ssyevd;
             char jz = jobz, ul = uplo;
             std::vector<float> wa(per);
             lint N = (lint)n, lwork = -1, liwork = -1, err = 0, liq = 0;
@@ -403,6 +523,7 @@ int oracle_svd(const float* a, uint32_t batch, uint32_t M, uint32_t N, float* u_
         std::vector<char> finite(batch);
         scan_matrices(a, batch, M, N, Part::all, amax.data(), finite.data());
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             char jz = jobz;
             lint lw = lwork, err = 0;
             std::vector<float> wa(per), tau(K), r(tall ? (size_t)K * K : 1), work(lwork);
@@ -458,6 +579,7 @@ int oracle_cholesky(const float* a, uint32_t batch, uint32_t n, int upper, float
         const size_t per = (size_t)n * n;
         const uint32_t ld = n >= 128 ? (n + 15) / 16 * 16 + 16 : n;
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             std::vector<float> w((size_t)n * ld, 0.0f);
             for (uint32_t b = b0; b < b1; ++b) {
                 const float* src = a + b * per;
@@ -501,6 +623,7 @@ int oracle_lu_factor(const float* a, uint32_t batch, uint32_t n, float* lu, uint
         const size_t per = (size_t)n * n;
         const uint32_t ld = padded_ld(n);
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             std::vector<float> w((size_t)n * ld);
             std::vector<lint> ipiv(n);
             for (uint32_t b = b0; b < b1; ++b) {
@@ -528,6 +651,7 @@ int oracle_solve(const float* a, uint32_t batch, uint32_t n, const float* bm, ui
         const size_t per = (size_t)n * n, bper = (size_t)n * nrhs;
         const uint32_t ld = padded_ld(n);
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             std::vector<float> w((size_t)n * ld), bw((size_t)nrhs * ld);
             std::vector<lint> ipiv(n);
             for (uint32_t b = b0; b < b1; ++b) {
@@ -560,6 +684,7 @@ int oracle_inv(const float* a, uint32_t batch, uint32_t n, float* x, uint32_t* i
         const uint32_t ld = padded_ld(n);
         const size_t lwork = (size_t)n * 64;
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             std::vector<float> w((size_t)n * ld), work(lwork);
             std::vector<lint> ipiv(n);
             for (uint32_t b = b0; b < b1; ++b) {
@@ -588,6 +713,7 @@ int oracle_solve_triangular(const float* a, uint32_t batch, uint32_t n, const fl
         const Lapack& L = g_lapack;
         const size_t per = (size_t)n * n, bper = (size_t)n * nrhs;
         lapack_batches(batch, [&](uint32_t b0, uint32_t b1) {
+            const Lapack& L = lap();
             for (uint32_t m = b0; m < b1; ++m) {
                 std::copy(b + m * bper, b + (m + 1) * bper, x + m * bper);
                 L.cblas_strsm(RowMajor, Left, upper ? Upper : Lower, NoTrans, unit ? Unit : NonUnit, (lint)n,
