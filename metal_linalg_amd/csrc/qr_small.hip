@@ -155,70 +155,106 @@ __device__ __forceinline__ float dot_from(const float* x, const float* y) {
     return (s0 + s1) + (s2 + s3);
 }
 
-// Factorization step J of the fixed-shape kernel (compile-time J, so every
-// row predicate folds away and only rows >= J are touched).  Lane J
-// publishes its column unscaled with the reflector's tau and scale (the
-// other lanes fold the scale into their products), and every lane scales its
-// own reflector once after the last step: one multiply per row instead of a
-// one-lane pass per step.  Square root and reciprocals are the hardware's,
-// the reciprocals refined by one Newton step.
-template <int J, int M, int N, int G, int LD>
-__device__ __forceinline__ void qr_fixed_step(float (&x)[M], float (&vsh)[LD], float* tsh, float* ssh, int c) {
-    if constexpr (J < (M < N ? M : N)) {
-        float ss = dot_from<J + 1, M>(x, x);
-        const float alpha = x[J];
-        float beta = alpha, tau = 0.0f, scale = 1.0f;
-        if (ss >= kTinySumsq) {
-            beta = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alpha, alpha, ss)), alpha);
-            tau = (beta - alpha) * rcp_refined(beta);
-            scale = rcp_refined(alpha - beta);
-        }
-        if (c == J) {
-            x[J] = beta;
-#pragma unroll
-            for (int r = J + 1; r < M; ++r) vsh[r] = x[r];
-            tsh[J] = tau;
-            ssh[J] = scale;
-        }
-        wave_lds_sync();
-        if (c > J) {
-            float v[M];
-#pragma unroll
-            for (int r = J + 1; r < M; ++r) v[r] = vsh[r];
-            const float sc = ssh[J];
-            const float d = tsh[J] * fmaf(sc, dot_from<J + 1, M>(v, x), x[J]);
-            const float ds = d * sc;
-            x[J] -= d;
-#pragma unroll
-            for (int r = J + 1; r < M; ++r) x[r] = fmaf(-ds, v[r], x[r]);
-        }
-        wave_lds_sync();
-        qr_fixed_step<J + 1, M, N, G, LD>(x, vsh, tsh, ssh, c);
+// The value of lane j of this lane's G-lane group, on every lane.
+template <int G>
+__device__ __forceinline__ float group_lane(float v, int j, int lane) {
+    if constexpr (G == 64) {
+        return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    } else if constexpr (G == 32) {
+        const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+        const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j + 32));
+        return lane >= 32 ? hi : lo;
+    } else {
+        return __shfl(v, (lane & ~(G - 1)) + j, 64);
     }
 }
 
-// Q formation step J (backward, sorg2r), for J = K-1 down to 0.
+// Rows LO .. M-1 of a column between registers and LDS as 16-byte pieces,
+// from the aligned row at or before LO (the rows before LO that this moves
+// are ignored by the reader).
+template <int LO, int M, int LD>
+__device__ __forceinline__ void put_rows(float (&vsh)[LD], const float (&x)[M]) {
+#pragma unroll
+    for (int r = LO / 4 * 4; r < M; r += 4)
+        *reinterpret_cast<float4*>(&vsh[r]) = make_float4(x[r], x[r + 1], x[r + 2], x[r + 3]);
+}
+template <int LO, int M, int LD>
+__device__ __forceinline__ void get_rows(float (&v)[M], const float (&vsh)[LD]) {
+#pragma unroll
+    for (int r = LO / 4 * 4; r < M; r += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(&vsh[r]);
+        v[r] = q.x;
+        v[r + 1] = q.y;
+        v[r + 2] = q.z;
+        v[r + 3] = q.w;
+    }
+}
+
+// Factorization step J of the fixed-shape kernel (compile-time J, so every
+// row predicate folds away and only rows >= J are touched).  Every lane
+// forms the reflector from lane J's column (alpha and the tail's sum of
+// squares read across lanes) with the hardware square root and refined
+// reciprocals; lane J publishes its column unscaled, the other lanes fold
+// the scale into their products, and each lane keeps the scale of its own
+// reflector to apply once after the last step.  Every lane runs the same
+// instructions, its part selected by a coefficient (zero for lanes at or
+// left of J): a divergent branch here would make the compiler copy the
+// column at every merge, as many moves as the step has multiply-adds.  The
+// lane index is laundered per step, or the compiler precomputes the lane
+// masks of every step at entry and spills them.
+template <int J, int M, int N, int G, int LD>
+__device__ __forceinline__ void qr_fixed_step(float (&x)[M], float (&vsh)[LD], float* tsh, int c, int lane,
+                                              float& myscale) {
+    if constexpr (J < (M < N ? M : N)) {
+        int cl = c;
+        __asm__ volatile("" : "+v"(cl));
+        const float alpha = group_lane<G>(x[J], J, lane);
+        const float ss = group_lane<G>(dot_from<J + 1, M>(x, x), J, lane);
+        const bool nz = ss >= kTinySumsq;
+        const float b = -copysignf(__builtin_amdgcn_sqrtf(fmaf(alpha, alpha, ss)), alpha);
+        const float beta = nz ? b : alpha;
+        const float tau = nz ? (b - alpha) * rcp_refined(b) : 0.0f;
+        const float sc = nz ? rcp_refined(alpha - b) : 1.0f;
+        if (cl == J) {   // stores only: no register changes inside
+            put_rows<J + 1, M, LD>(vsh, x);
+            tsh[J] = tau;
+        }
+        myscale = cl == J ? sc : myscale;
+        wave_lds_sync();
+        float v[M];
+        get_rows<J + 1, M, LD>(v, vsh);
+        const float d0 = tau * fmaf(sc, dot_from<J + 1, M>(v, x), x[J]);
+        const float d = cl > J ? d0 : 0.0f;
+        const float ds = d * sc;
+        x[J] = cl == J ? beta : x[J] - d;
+#pragma unroll
+        for (int r = J + 1; r < M; ++r) x[r] = fmaf(-ds, v[r], x[r]);
+        wave_lds_sync();
+        qr_fixed_step<J + 1, M, N, G, LD>(x, vsh, tsh, c, lane, myscale);
+    }
+}
+
+// Q formation step J (backward, sorg2r), for J = K-1 down to 0.  Lane J
+// holds its reflector v (1 at row J, zero above, set before the first step)
+// and becomes e_J - tau v; lanes right of J lose tau (v . x) v; the others
+// keep their column.  In one form for every lane: x - beta v, plus 1 at row
+// J in lane J, with beta = tau + 1 in lane J (x = v there), tau (v . x)
+// right of J and 0 left of it.
 template <int J, int M, int K, int LD>
 __device__ __forceinline__ void qr_fixed_qstep(float (&x)[M], float (&vsh)[LD], const float* tsh, int c, int qc) {
     if constexpr (J >= 0) {
-        if (c == J) {
-            vsh[J] = 1.0f;
-#pragma unroll
-            for (int r = J + 1; r < M; ++r) vsh[r] = x[r];
-        }
+        int cl = c;
+        __asm__ volatile("" : "+v"(cl));
+        if (cl == J) put_rows<J, M, LD>(vsh, x);
         wave_lds_sync();
         const float t = tsh[J];
-        if (c > J && c < qc) {
-            float v[M];
+        float v[M];
+        get_rows<J, M, LD>(v, vsh);
+        const float dot = t * dot_from<J, M>(v, x);
+        const float beta = cl == J ? t + 1.0f : (cl > J && cl < qc ? dot : 0.0f);
 #pragma unroll
-            for (int r = J; r < M; ++r) v[r] = vsh[r];
-            const float d = t * dot_from<J, M>(v, x);
-#pragma unroll
-            for (int r = J; r < M; ++r) x[r] = fmaf(-d, v[r], x[r]);
-        } else if (c == J) {
-#pragma unroll
-            for (int r = 0; r < M; ++r) x[r] = r < J ? 0.0f : (r == J ? 1.0f - t : -t * x[r]);
-        }
+        for (int r = J; r < M; ++r) x[r] = fmaf(-beta, v[r], x[r]);
+        x[J] += cl == J ? 1.0f : 0.0f;
         wave_lds_sync();
         qr_fixed_qstep<J - 1, M, K, LD>(x, vsh, tsh, c, qc);
     }
@@ -226,15 +262,17 @@ __device__ __forceinline__ void qr_fixed_qstep(float (&x)[M], float (&vsh)[LD], 
 
 // Fixed-shape variant for M >= N known at compile time (the hot batched
 // shapes): the column loop is unrolled, so row predicates vanish and step j
-// touches rows j.. only.  qc is 0 (R alone) or N.
+// touches rows j.. only.  qc is 0 (R alone) or N.  (Two groups of matrices
+// per wave, the second's loads in flight during the first's arithmetic, ran
+// slower at config 1: 82.9 against 71.2 us, the lower occupancy costing more
+// than the overlap gained.)
 template <int M, int N, int G>
 __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ A, float* __restrict__ Q,
                                                       float* __restrict__ Rout, uint32_t batch, uint32_t qc) {
     constexpr int MPW = 64 / G;
-    constexpr int LD = M + 4;   // per-group stride, off the other group's banks
+    constexpr int LD = M + 4;   // per-group stride (16-byte multiple), off the other group's banks
     __shared__ float vsh[MPW][LD];
     __shared__ float tsh[MPW][N];
-    __shared__ float ssh[MPW][N];   // the reflectors' scales
     const int lane = threadIdx.x;
     const int c = lane % G;
     const int g = lane / G;
@@ -259,12 +297,11 @@ __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ 
 #pragma unroll
     for (int r = 0; r < M; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
 
-    qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], ssh[g], c);
-    {   // lane c's reflector below the diagonal, scaled now
-        const float sc = ssh[g][c < N ? c : 0];
+    float myscale = 1.0f;
+    qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], c, lane, myscale);
+    // lane c's reflector below the diagonal, scaled now
 #pragma unroll
-        for (int r = 0; r < M; ++r) x[r] = r > c ? x[r] * sc : x[r];
-    }
+    for (int r = 0; r < M; ++r) x[r] = r > c ? x[r] * myscale : x[r];
 
     if (live && c < N) {
         float* out_r = Rout + mat * N * N;
@@ -273,6 +310,10 @@ __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ 
         for (int r = 0; r < N; ++r) out_r[(size_t)r * N + c] = bad ? qnan() : (c >= r ? x[r] * unscale : 0.0f);
     }
     if (qc == 0) return;
+    // lane c's column becomes its reflector: 1 at row c, zero above (the
+    // columns of a square Q past K do not exist here: M >= N = K)
+#pragma unroll
+    for (int r = 0; r < M; ++r) x[r] = r < c ? 0.0f : (r == c ? 1.0f : x[r]);
     qr_fixed_qstep<N - 1, M, N, LD>(x, vsh[g], tsh[g], c, (int)qc);
     if (live && c < N) {
         float* out_q = Q + mat * M * N;
