@@ -246,6 +246,69 @@ def workloads():
     return w
 
 
+def _arrays(x):
+    if x is None:
+        return []
+    if isinstance(x, dict):
+        return [v for v in x.values() if hasattr(v, "nbytes")]
+    if isinstance(x, (tuple, list)):
+        return [v for v in x if v is not None and hasattr(v, "nbytes")]
+    return [x] if hasattr(x, "nbytes") else []
+
+
+def host_pointer_path(wl, api, host, reps):
+    """The call on host (numpy) buffers: staged through pinned memory in
+    chunks by the library.  Beside it, the PCIe bound for the same bytes:
+    pinned torch copies of the inputs to the device and of the outputs back,
+    the two directions on two streams at once (the link is full duplex)."""
+    import torch
+
+    out = wl.call(api, host)   # warm-up: pinned and device staging allocated
+    in_bytes = sum(a.nbytes for a in _arrays(host))
+    out_bytes = sum(a.nbytes for a in _arrays(out))
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        wl.call(api, host)
+    t_call = (time.perf_counter() - t0) / reps
+    # the caller's buffers pinned (torch pin_memory tensors in and out): the
+    # transfers read and write them directly
+    pinned = {k: (torch.from_numpy(v).pin_memory() if isinstance(v, np.ndarray) else v) for k, v in host.items()}
+    wl.call(api, pinned)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        wl.call(api, pinned)
+    t_pinned = (time.perf_counter() - t0) / reps
+    h_in = torch.empty(max(1, in_bytes), dtype=torch.uint8, pin_memory=True)
+    d_in = torch.empty(max(1, in_bytes), dtype=torch.uint8, device="cuda")
+    d_out = torch.empty(max(1, out_bytes), dtype=torch.uint8, device="cuda")
+    h_out = torch.empty(max(1, out_bytes), dtype=torch.uint8, pin_memory=True)
+    s_up, s_down = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def both():
+        with torch.cuda.stream(s_up):
+            d_in.copy_(h_in, non_blocking=True)
+        with torch.cuda.stream(s_down):
+            h_out.copy_(d_out, non_blocking=True)
+
+    both()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        both()
+    torch.cuda.synchronize()
+    t_pcie = (time.perf_counter() - t0) / reps
+    total = in_bytes + out_bytes
+    return {"value": round(wl.rate(1, t_call), 2), "unit": wl.unit, "ms_per_call": round(t_call * 1e3, 3),
+            "host_bytes_per_call": total, "gb_s": round(total / t_call / 1e9, 2),
+            "pcie_bound": {"ms_per_call": round(t_pcie * 1e3, 3), "gb_s": round(total / t_pcie / 1e9, 2),
+                           "rate": round(wl.rate(1, t_pcie), 2),
+                           "how": "pinned torch copies of the same bytes, inputs up and outputs down at once"},
+            "frac_of_pcie_bound": round(t_pcie / t_call, 4),
+            "pinned_buffers": {"value": round(wl.rate(1, t_pinned), 2), "ms_per_call": round(t_pinned * 1e3, 3),
+                               "gb_s": round(total / t_pinned / 1e9, 2),
+                               "frac_of_pcie_bound": round(t_pcie / t_pinned, 4)}}
+
+
 def host_cpus() -> str:
     """The CPU model and the cores this process may run on."""
     model = ""
@@ -373,11 +436,7 @@ def main():
                               "frac": round(issue_s / kernel_s_per_call, 4)}
 
     # host-pointer (PCIe-inclusive) rate, for the record; never `value`
-    t0 = time.perf_counter()
-    reps = max(1, min(5, args.steps))
-    for _ in range(reps):
-        wl.call(api, host)
-    host_rate = wl.rate(reps, time.perf_counter() - t0)
+    host_path = host_pointer_path(wl, api, host, max(1, min(5, args.steps)))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -399,7 +458,8 @@ def main():
         "config": dict({"workload": wl.desc}, **wl.shape),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "host_pointer_rate": round(host_rate, 2),
+        "host_pointer_rate": host_path["value"],
+        "host_pointer": host_path,
         "kernels": {k: {"launches": v[0], "total_ms": round(v[1], 4)} for k, v in other.items()},
         "device": _lib.device_name().decode(),
         "arch": _lib.hip_arch().decode(),

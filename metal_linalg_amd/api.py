@@ -39,6 +39,9 @@ class _Arrays:
                 a = a.to(torch.float32)
             self.a = a.contiguous()
             self.device = self.a.device
+            # pinned host input -> pinned host outputs: the library then moves
+            # them over PCIe directly, with no copy through its own staging
+            self.pinned = self.device.type == "cpu" and self.a.is_pinned()
         else:
             self.a = np.ascontiguousarray(a, dtype=np.float32)
         self.keep = [self.a]
@@ -50,6 +53,8 @@ class _Arrays:
             if not _is_torch(x):
                 x = torch.as_tensor(x)
             x = x.to(device=self.device, dtype=torch.float32).contiguous()
+            if self.pinned and not x.is_pinned():
+                x = x.pin_memory()
         else:
             x = np.ascontiguousarray(x, dtype=np.float32)
         self.keep.append(x)
@@ -60,7 +65,10 @@ class _Arrays:
             import torch
 
             dt = torch.float32 if dtype == "f32" else torch.int32
-            x = torch.empty(shape, dtype=dt, device=self.device)
+            if self.pinned:
+                x = torch.empty(shape, dtype=dt, pin_memory=True)
+            else:
+                x = torch.empty(shape, dtype=dt, device=self.device)
         else:
             x = np.empty(shape, dtype=np.float32 if dtype == "f32" else np.uint32)
         self.keep.append(x)

@@ -31,6 +31,9 @@ namespace mla::core {
 
 namespace {
 
+float* f32(void* p) { return static_cast<float*>(p); }
+uint32_t* u32p(void* p) { return static_cast<uint32_t*>(p); }
+
 __global__ void fill_identity_kernel(float* q, uint64_t batch, uint32_t m) {
     const uint64_t per = (uint64_t)m * m;
     const uint64_t total = batch * per;
@@ -62,15 +65,20 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
         invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) +
                 ": this build's QR kernels take at most 4096 rows so far");
     Call call;
+    if (small) {
+        call.batched(B, {{a.data, nullptr, (size_t)M * N * 4}, {nullptr, QC ? q : nullptr, (size_t)M * QC * 4},
+                         {nullptr, r, (size_t)RR * N * 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         qr_small(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, QC, RR, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * M * N);
     float* dq = QC ? call.out(q, (size_t)B * M * QC) : nullptr;
     float* dr = call.out(r, (size_t)B * RR * N);
-    if (small) {
-        qr_small(da, dq, dr, B, M, N, QC, RR, call.stream());
-    } else {
-        float* work = static_cast<float*>(call.scratch(qr_blocked_workspace(M, N)));
-        qr_blocked(da, dq, dr, B, M, N, QC, RR, work, call.stream());
-    }
+    float* work = static_cast<float*>(call.scratch(qr_blocked_workspace(M, N)));
+    qr_blocked(da, dq, dr, B, M, N, QC, RR, work, call.stream());
     call.finish();
 }
 
@@ -79,10 +87,7 @@ namespace {
 // A finite matrix that did not converge is an error (reference:
 // src/eigh_ql.mm:254-262, src/svd_golub_kahan.mm:349-362): the info words
 // are read back and checked.
-void check_converged(const uint32_t* dinfo, uint32_t batch, hipStream_t s, const char* what) {
-    std::vector<uint32_t> h(batch);
-    MLA_HIP(hipMemcpyAsync(h.data(), dinfo, (size_t)batch * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-    MLA_HIP(hipStreamSynchronize(s));
+void check_converged_host(const uint32_t* h, uint32_t batch, const char* what) {
     for (uint32_t b = 0; b < batch; ++b) {
         const uint32_t i = h[b];
         if (!((i >> 17) & 1u) && !((i >> 16) & 1u))
@@ -90,6 +95,13 @@ void check_converged(const uint32_t* dinfo, uint32_t batch, hipStream_t s, const
                                      std::to_string(batch) + " did not converge (" + std::to_string(i & 0xFFFFu) +
                                      " iterations).");
     }
+}
+
+void check_converged(const uint32_t* dinfo, uint32_t batch, hipStream_t s, const char* what) {
+    std::vector<uint32_t> h(batch);
+    MLA_HIP(hipMemcpyAsync(h.data(), dinfo, (size_t)batch * sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    MLA_HIP(hipStreamSynchronize(s));
+    check_converged_host(h.data(), batch, what);
 }
 
 }  // namespace
@@ -113,18 +125,27 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
     if (!small && !eigh_blocked_fits(n))
         invalid("[eigh] n = " + std::to_string(n) + ": this build's eigh kernels take n <= 16384");
     Call call;
-    const float* da = call.in(a.data, (size_t)B * n * n);
-    float* dw = call.out(w, (size_t)B * n);
-    float* dv = v ? call.out(v, (size_t)B * n * n) : nullptr;
-    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
     if (small) {
         // no convergence read-back: bisection always ends (every info word
         // carries bit 16, or bit 17 for a non-finite matrix), so the
         // reference's non-convergence error cannot arise on this path
-        const size_t wsb = eigh_small_workspace(n, B, dv != nullptr);
+        const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)n * n * 4},
+                                             {nullptr, w, (size_t)n * 4},
+                                             {nullptr, v, v ? (size_t)n * n * 4 : 0},
+                                             {nullptr, info, 4}};
+        const size_t wsb = eigh_small_workspace(n, call.chunk_size(B, sl), v != nullptr);
         float* ws = wsb ? static_cast<float*>(call.scratch(wsb)) : nullptr;
-        eigh_small(da, dw, dv, di, B, n, lower, ws, call.stream());
-    } else {
+        call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t s) {
+            eigh_small(f32(d[0]), f32(d[1]), f32(d[2]), u32p(d[3]), nb, n, lower, ws, s);
+        });
+        call.finish();
+        return;
+    }
+    const float* da = call.in(a.data, (size_t)B * n * n);
+    float* dw = call.out(w, (size_t)B * n);
+    float* dv = v ? call.out(v, (size_t)B * n * n) : nullptr;
+    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
+    {
         const size_t floats = eigh_sytrd_floats(n) + eigh_tridiag_floats(n);
         float* work = static_cast<float*>(call.scratch(floats * sizeof(float)));
         const EighWork ew = eigh_carve(work, n);
@@ -252,14 +273,20 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
         return;
     }
     Call call;
-    const float* da = call.in(a.data, (size_t)B * M * N);
-    float* ds = call.out(s, (size_t)B * K);
-    float* du = u ? call.out(u, (size_t)B * M * K) : nullptr;
-    float* dvt = vt ? call.out(vt, (size_t)B * K * N) : nullptr;
-    uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
-    float* ws = static_cast<float*>(call.scratch(svd_small_workspace(M, N, B)));
-    svd_small(da, du, ds, dvt, di, ws, B, M, N, call.stream());
-    check_converged(di, B, call.stream(), "svd");
+    // the info words are read back for the convergence check: the caller's
+    // array (host or device) or a device one
+    uint32_t* ibuf = info ? info : call.tmp<uint32_t>(B);
+    const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)M * N * 4},
+                                         {nullptr, u, u ? (size_t)M * K * 4 : 0},
+                                         {nullptr, s, (size_t)K * 4},
+                                         {nullptr, vt, vt ? (size_t)K * N * 4 : 0},
+                                         {nullptr, ibuf, 4}};
+    float* ws = static_cast<float*>(call.scratch(svd_small_workspace(M, N, call.chunk_size(B, sl))));
+    call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t st) {
+        svd_small(f32(d[0]), f32(d[1]), f32(d[2]), f32(d[3]), u32p(d[4]), ws, nb, M, N, st);
+    });
+    if (is_device_memory(ibuf)) check_converged(ibuf, B, call.stream(), "svd");
+    else check_converged_host(ibuf, B, "svd");
     call.finish();
 }
 
@@ -285,12 +312,17 @@ void cholesky(const Matrices& a, bool upper, float* l, uint32_t* info) {
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0) return;
     Call call;
+    if (chol_small_fits(n)) {
+        call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, l, (size_t)n * n * 4}, {nullptr, info, 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         chol_small(f32(d[0]), f32(d[1]), u32p(d[2]), nb, n, upper, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dl = call.out(l, (size_t)B * n * n);
-    if (chol_small_fits(n)) {
-        uint32_t* di = call.out(info, B);
-        chol_small(da, dl, di, B, n, upper, call.stream());
-    } else {
+    {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
         float* work = static_cast<float*>(call.scratch(chol_blocked_workspace(n)));
         chol_blocked(da, dl, di, work, work + (size_t)n * n, B, n, upper, call.stream());
@@ -306,13 +338,19 @@ void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
     if (n == 0 || B == 0) return;
     if (!lu_blocked_fits(n)) too_large("lu_factor", n, 16384);
     Call call;
+    if (lu_small_factor_fits(n)) {
+        call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, lu, (size_t)n * n * 4},
+                         {nullptr, pivots, (size_t)n * 4}, {nullptr, info, 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         lu_small_factor(f32(d[0]), f32(d[1]), u32p(d[2]), u32p(d[3]), nb, n, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dlu = call.out(lu, (size_t)B * n * n);
     uint32_t* dp = call.out(pivots, (size_t)B * n);
-    if (lu_small_factor_fits(n)) {
-        uint32_t* di = call.out(info, B);
-        lu_small_factor(da, dlu, dp, di, B, n, call.stream());
-    } else {
+    {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
         float* work = static_cast<float*>(call.scratch(lu_panel_workspace(n)));
         lu_blocked_factor(da, dlu, dp, di, work, B, n, call.stream());
@@ -335,13 +373,19 @@ void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t*
     }
     if (!lu_blocked_fits(n)) too_large("solve", n, 16384);
     Call call;
+    if (lu_small_factor_fits(n)) {
+        call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {b, nullptr, (size_t)n * nrhs * 4},
+                         {nullptr, x, (size_t)n * nrhs * 4}, {nullptr, info, 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         lu_small_solve(f32(d[0]), f32(d[1]), nrhs, f32(d[2]), u32p(d[3]), nb, n, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    if (lu_small_factor_fits(n)) {
-        uint32_t* di = call.out(info, B);
-        lu_small_solve(da, db, nrhs, dx, di, B, n, call.stream());
-    } else {
+    {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
         float* work = static_cast<float*>(call.scratch(lu_blocked_workspace(n)));
         // the blocked path gathers b's rows into x: an x that overlaps b
@@ -365,12 +409,17 @@ void inv(const Matrices& a, float* x, uint32_t* info) {
     if (n == 0 || B == 0) return;
     if (!lu_blocked_fits(n)) too_large("inv", n, 16384);
     Call call;
+    if (lu_small_factor_fits(n)) {
+        call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, x, (size_t)n * n * 4}, {nullptr, info, 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         lu_small_inv(f32(d[0]), f32(d[1]), u32p(d[2]), nb, n, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * n * n);
     float* dx = call.out(x, (size_t)B * n * n);
-    if (lu_small_factor_fits(n)) {
-        uint32_t* di = call.out(info, B);
-        lu_small_inv(da, dx, di, B, n, call.stream());
-    } else {
+    {
         uint32_t* di = info ? call.out(info, B) : call.tmp<uint32_t>(B);
         float* work = static_cast<float*>(call.scratch(lu_blocked_workspace(n)));
         lu_blocked_solve(da, nullptr, n, dx, di, work, B, n, call.stream());
@@ -385,12 +434,19 @@ void solve_triangular(const Matrices& a, const float* b, uint32_t nrhs, bool upp
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0 || nrhs == 0) return;
     Call call;
+    if (lu_small_factor_fits(n)) {   // the triangular solve takes the same n
+        call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {b, nullptr, (size_t)n * nrhs * 4},
+                         {nullptr, x, (size_t)n * nrhs * 4}},
+                     [&](void* const* d, uint32_t nb, hipStream_t s) {
+                         trsm_small(f32(d[0]), f32(d[1]), f32(d[2]), nb, n, nrhs, upper, unit, s);
+                     });
+        call.finish();
+        return;
+    }
     const float* da = call.in(a.data, (size_t)B * n * n);
     const float* db = call.in(b, (size_t)B * n * nrhs);
     float* dx = call.out(x, (size_t)B * n * nrhs);
-    if (lu_small_factor_fits(n)) {   // the triangular solve takes the same n
-        trsm_small(da, db, dx, B, n, nrhs, upper, unit, call.stream());
-    } else {
+    {
         if (dx != db)
             MLA_HIP(hipMemcpyAsync(dx, db, (size_t)B * n * nrhs * sizeof(float), hipMemcpyDeviceToDevice,
                                    call.stream()));

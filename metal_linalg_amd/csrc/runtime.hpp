@@ -12,6 +12,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -67,6 +68,30 @@ public:
 
     // Waits for the kernels, copies host outputs back, checks for errors.
     void finish();
+
+    // ---- batched calls of independent matrices ----
+    // One caller buffer of a batched call: an input (`in`) or an output
+    // (`out`, NULL allowed), `per` bytes per matrix.
+    struct Slice {
+        const void* in = nullptr;
+        void* out = nullptr;
+        size_t per = 0;
+    };
+    // Device pointers of a chunk's slices (in the order given), the chunk's
+    // matrix count and the stream to launch on.
+    using ChunkLaunch = std::function<void(void* const* dev, uint32_t count, hipStream_t s)>;
+    // Matrices per launch that batched() will use: the whole batch when
+    // every buffer is device memory, else a chunk of about kChunkBytes of
+    // host traffic.  Size per-launch scratch with it.
+    uint32_t chunk_size(uint32_t batch, const std::vector<Slice>& slices) const;
+    // Runs a batched call.  Device buffers are used in place and the whole
+    // batch is one launch.  When any buffer is host memory the batch runs in
+    // chunks through pinned staging buffers, two chunks in flight: the host
+    // copies of one chunk, the transfers of another and the kernels of a
+    // third overlap (uploads and downloads on two more streams, ordered by
+    // events).  Every
+    // host output is written when this returns; finish() still follows.
+    void batched(uint32_t batch, const std::vector<Slice>& slices, const ChunkLaunch& launch);
 
 private:
     std::unique_lock<std::mutex> lock_;
