@@ -103,18 +103,31 @@ def _qr_setup(ctx, inputs, output):
     ctx.save_for_backward(q, r)
 
 
+def _qr_tall_grad(q, r, gq, gr):
+    """A = Q R with M >= N (R square, invertible): gA = (gQ + Q copyltu(M)) R^-T,
+    M = R gR^T - gQ^T Q."""
+    mm = r @ gr.mT.contiguous() - gq.mT.contiguous() @ q
+    b = gq + q @ _copyltu(mm)
+    return torch.linalg.solve_triangular(r, b.mT.contiguous(), upper=True, left=True).mT
+
+
 def _qr_backward(ctx, gq, gr):
     q, r = ctx.saved_tensors
     m, n = q.shape[-2], r.shape[-1]
-    if ctx.mode != "reduced" or m < n:
-        raise NotImplementedError("metal_linalg.qr: the backward is defined for mode='reduced' with M >= N")
+    if ctx.mode != "reduced":
+        raise NotImplementedError("metal_linalg.qr: the backward is defined for mode='reduced'")
     gq = torch.zeros_like(q) if gq is None else gq
     gr = torch.zeros_like(r) if gr is None else gr
-    # A = Q R: gA = (gQ + Q copyltu(M)) R^-T, M = R gR^T - gQ^T Q
-    mm = r @ gr.mT.contiguous() - gq.mT.contiguous() @ q
-    b = gq + q @ _copyltu(mm)
-    ga = torch.linalg.solve_triangular(r, b.mT.contiguous(), upper=True, left=True).mT
-    return ga.contiguous(), None
+    if m >= n:
+        return _qr_tall_grad(q, r, gq, gr).contiguous(), None
+    # wide: A = [X Y] with X = Q R1 (square) and Y = Q R2, R2 = Q^T Y.  Y's
+    # part: gY = Q gR2; through R2 the loss also depends on Q: gQ += Y gR2^T.
+    r1, r2 = r[..., :m], r[..., m:]
+    gr1, gr2 = gr[..., :m], gr[..., m:]
+    y = q @ r2
+    gx = _qr_tall_grad(q, r1, gq + y @ gr2.mT.contiguous(), gr1)
+    gy = q @ gr2
+    return torch.cat([gx, gy], dim=-1).contiguous(), None
 
 
 qr.register_autograd(_qr_backward, setup_context=_qr_setup)

@@ -90,6 +90,10 @@ def test_gradients(cuda):
     print("qr")
     g, r = _grads(lambda t: [sq(y) for y in ops.qr(t)], lambda t: [sq(y) for y in torch.linalg.qr(t)], x, 11)
     _close(g, r, 2e-3)
+    print("qr wide")
+    wide = _rand((3, 5, 8), 5)
+    g, r = _grads(lambda t: [sq(y) for y in ops.qr(t)], lambda t: [sq(y) for y in torch.linalg.qr(t)], wide, 20)
+    _close(g, r, 2e-3)
     print("svd")
     g, r = _grads(lambda t: [sq(y) for y in ops.svd(t)], lambda t: [sq(y) for y in torch.linalg.svd(t, full_matrices=False)],
                   x, 12)
