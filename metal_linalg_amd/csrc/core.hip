@@ -3,11 +3,13 @@
 #include "core.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "kernels.hpp"
+#include "policy.hpp"
 #include "runtime.hpp"
 
 namespace mla {
@@ -292,6 +294,13 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
 
 namespace {
 
+// LU, solve and inverse: the batched kernels unless the route is the
+// blocked path (the reference's "cpu" route is its batch path, which is the
+// batched kernels here)
+bool lu_batched(uint32_t n, uint32_t batch) {
+    return lu_small_factor_fits(n) && std::strcmp(lu_backend_name(n, batch), "blocked") != 0;
+}
+
 void require_square(const Matrices& a, const char* what) {
     if (a.rows != a.cols)
         invalid(std::string("[") + what + "] The matrices must be square, got " + std::to_string(a.rows) + "x" +
@@ -312,7 +321,9 @@ void cholesky(const Matrices& a, bool upper, float* l, uint32_t* info) {
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0) return;
     Call call;
-    if (chol_small_fits(n)) {
+    // the routed backend: the batched kernels ("simd", "threadgroup"; also a
+    // "cpu" route, this build's batch path) or the blocked path
+    if (chol_small_fits(n) && std::strcmp(cholesky_backend_name(n, B), "blocked") != 0) {
         call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, l, (size_t)n * n * 4}, {nullptr, info, 4}},
                      [&](void* const* d, uint32_t nb, hipStream_t s) {
                          chol_small(f32(d[0]), f32(d[1]), u32p(d[2]), nb, n, upper, s);
@@ -338,7 +349,7 @@ void lu_factor(const Matrices& a, float* lu, uint32_t* pivots, uint32_t* info) {
     if (n == 0 || B == 0) return;
     if (!lu_blocked_fits(n)) too_large("lu_factor", n, 16384);
     Call call;
-    if (lu_small_factor_fits(n)) {
+    if (lu_batched(n, B)) {
         call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, lu, (size_t)n * n * 4},
                          {nullptr, pivots, (size_t)n * 4}, {nullptr, info, 4}},
                      [&](void* const* d, uint32_t nb, hipStream_t s) {
@@ -373,7 +384,7 @@ void solve(const Matrices& a, const float* b, uint32_t nrhs, float* x, uint32_t*
     }
     if (!lu_blocked_fits(n)) too_large("solve", n, 16384);
     Call call;
-    if (lu_small_factor_fits(n)) {
+    if (lu_batched(n, B)) {
         call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {b, nullptr, (size_t)n * nrhs * 4},
                          {nullptr, x, (size_t)n * nrhs * 4}, {nullptr, info, 4}},
                      [&](void* const* d, uint32_t nb, hipStream_t s) {
@@ -409,7 +420,7 @@ void inv(const Matrices& a, float* x, uint32_t* info) {
     if (n == 0 || B == 0) return;
     if (!lu_blocked_fits(n)) too_large("inv", n, 16384);
     Call call;
-    if (lu_small_factor_fits(n)) {
+    if (lu_batched(n, B)) {
         call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {nullptr, x, (size_t)n * n * 4}, {nullptr, info, 4}},
                      [&](void* const* d, uint32_t nb, hipStream_t s) {
                          lu_small_inv(f32(d[0]), f32(d[1]), u32p(d[2]), nb, n, s);
@@ -434,7 +445,8 @@ void solve_triangular(const Matrices& a, const float* b, uint32_t nrhs, bool upp
     const uint32_t n = a.cols, B = a.batch;
     if (n == 0 || B == 0 || nrhs == 0) return;
     Call call;
-    if (lu_small_factor_fits(n)) {   // the triangular solve takes the same n
+    // the triangular solve takes the same n; the routed backend as LU's
+    if (lu_small_factor_fits(n) && std::strcmp(trsm_backend_name(n, nrhs, B), "blocked") != 0) {
         call.batched(B, {{a.data, nullptr, (size_t)n * n * 4}, {b, nullptr, (size_t)n * nrhs * 4},
                          {nullptr, x, (size_t)n * nrhs * 4}},
                      [&](void* const* d, uint32_t nb, hipStream_t s) {

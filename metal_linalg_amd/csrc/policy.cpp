@@ -18,6 +18,7 @@
 
 #include "core.hpp"
 #include "runtime.hpp"
+#include "tuned_gfx950.inc"
 
 namespace mla {
 namespace {
@@ -418,6 +419,9 @@ State<metal_linalg_cholesky_policy>& cholesky_state() {
             p.gpu_min_batch = 1;
             p.gpu_min_n = 0;
             p.gpu_large_min_n = 0;
+            // batched kernels ("simd", "threadgroup") against the blocked path
+            p.blocked_min_n = tuned::kCholeskyBlockedMinN;
+            p.blocked_max_batch = tuned::kCholeskyBlockedMaxBatch;
             r.source = tuned_label();
         } else {
             r.source = untuned_label();
@@ -447,8 +451,10 @@ State<metal_linalg_lu_policy>& lu_state() {
         p = {2048, 0, 16, 0};   // reference defaults (core.h LuPolicy)
         p.gpu_cores = device_id().cus;
         if (device_id().mi355x) {
-            p.gpu_min_n = 1;   // every shape on the GPU
-            p.gpu_max_batch = 0;
+            // "blocked": the one-matrix-at-a-time blocked path; "cpu": the
+            // batch path, which on this device is the batched GPU kernels
+            p.gpu_min_n = tuned::kLuBlockedMinN;
+            p.gpu_max_batch = tuned::kLuBlockedMaxBatch;
             p.gpu_solve_min_rhs = 1;
             r.source = tuned_label();
         } else {
@@ -473,9 +479,10 @@ State<metal_linalg_trsm_policy>& trsm_state() {
         p = {1024, 256, 0, 0};   // reference defaults (core.h TrsmPolicy)
         p.gpu_cores = device_id().cus;
         if (device_id().mi355x) {
-            p.gpu_min_n = 1;   // every shape on the GPU
+            // as LU's: "blocked" the blocked path, "cpu" the batched kernels
+            p.gpu_min_n = tuned::kTrsmBlockedMinN;
             p.gpu_min_rhs = 0;
-            p.gpu_max_batch = 0;
+            p.gpu_max_batch = tuned::kTrsmBlockedMaxBatch;
             r.source = tuned_label();
         } else {
             r.source = untuned_label();
