@@ -63,16 +63,23 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
     }
     if (K == 0 || B == 0) return;
     const bool small = qr_small_fits(M, N, QC);
-    if (!small && !qr_blocked_fits(M, N))
+    // tall matrices of at most 64 columns: the batched tall kernel (a tree
+    // of 128-row blocks past 128 rows)
+    const bool tall = !small && qr_tall_fits(M, N, QC);
+    if (!small && !tall && !qr_blocked_fits(M, N))
         invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) +
-                ": this build's QR kernels take at most 4096 rows so far");
+                ": this build's QR kernels take at most 4096 rows beyond 64 columns");
     Call call;
-    if (small) {
-        call.batched(B, {{a.data, nullptr, (size_t)M * N * 4}, {nullptr, QC ? q : nullptr, (size_t)M * QC * 4},
-                         {nullptr, r, (size_t)RR * N * 4}},
-                     [&](void* const* d, uint32_t nb, hipStream_t s) {
-                         qr_small(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, QC, RR, s);
-                     });
+    if (small || tall) {
+        const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)M * N * 4},
+                                             {nullptr, QC ? q : nullptr, (size_t)M * QC * 4},
+                                             {nullptr, r, (size_t)RR * N * 4}};
+        const size_t wsb = tall ? qr_tall_workspace(M, N, call.chunk_size(B, sl), QC != 0) : 0;
+        float* ws = wsb ? static_cast<float*>(call.scratch(wsb)) : nullptr;
+        call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t s) {
+            if (small) qr_small(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, QC, RR, s);
+            else qr_tall(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, ws, s);
+        });
         call.finish();
         return;
     }
@@ -188,7 +195,7 @@ void batch_transpose(const float* src, float* dst, uint32_t batch, uint32_t rows
 }
 
 // Thin SVD of matrices with min(M, N) = K <= 64 beyond the batched kernel's
-// 128 rows: the tall problem A = Q R (blocked Householder QR), the SVD of the
+// 128 rows: the tall problem A = Q R (the batched tall QR), the SVD of the
 // K x K factor R = U_R S V^T (batched kernel), then U = Q U_R (MFMA GEMM).
 // A wide matrix is solved as its transpose.  Non-finite input reaches R as
 // NaN and gives NaN outputs with info bit 17; the flag bits and sweep counts
@@ -215,8 +222,9 @@ void svd_tall(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) 
     }
     float* q = vec ? call.tmp<float>((size_t)B * m * k) : nullptr;
     float* r = call.tmp<float>((size_t)B * k * k);
-    float* qw = static_cast<float*>(call.scratch(qr_blocked_workspace(m, k)));
-    qr_blocked(tall, q, r, B, m, k, vec ? k : 0, k, qw, st);
+    const size_t qwb = qr_tall_workspace(m, k, B, vec);
+    float* qw = qwb ? static_cast<float*>(call.scratch(qwb)) : nullptr;
+    qr_tall(tall, q, r, B, m, k, qw, st);
     float* ur = vec ? call.tmp<float>((size_t)B * k * k) : nullptr;
     // right vectors of the tall problem: A's V^T, or (wide) A's U transposed
     float* vtt = !vec ? nullptr : wide ? call.tmp<float>((size_t)B * k * k) : dvt;
@@ -253,7 +261,7 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
         return;
     }
     if (!svd_small_fits(M, N)) {
-        if (K <= 64 && qr_blocked_fits(std::max(M, N), K)) {
+        if (K <= 64) {
             svd_tall(a, u, s, vt, info);
             return;
         }

@@ -16,6 +16,14 @@ bool qr_small_fits(uint32_t m, uint32_t n, uint32_t qc);
 void qr_small(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
               hipStream_t s);
 
+// ---- QR of tall matrices: n <= 64 columns, any m >= n rows, batched ----
+// Reduced mode (q [batch, m, n]) or R alone (q NULL); r [batch, n, n].
+// work = qr_tall_workspace(m, n, batch, q != NULL) bytes (none up to 128 rows).
+bool qr_tall_fits(uint32_t m, uint32_t n, uint32_t qc);
+size_t qr_tall_workspace(uint32_t m, uint32_t n, uint32_t batch, bool with_q);
+void qr_tall(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, float* work,
+             hipStream_t s);
+
 // ---- QR for larger matrices (m <= 4096), one matrix at a time ----
 // work = qr_blocked_workspace(m, n) bytes; q may be NULL when qc = 0.
 bool qr_blocked_fits(uint32_t m, uint32_t n);
