@@ -187,6 +187,41 @@ def workloads():
         8192 * (1024 + 256 + 256), 8192 * 1024, "hbm",
         lambda o, h, n: o.solve_triangular(h["a"][:n], h["b"][:n], False, True), {"batch": 8192, "n": 16, "nrhs": 4})
 
+    # the batched tall QR (one wave per block of up to 128 rows, a reduction
+    # tree of block QRs beyond): the reference's QR window past its register
+    # kernel, 65 to 4096 rows with at most 64 columns
+    def tall_make(batch, m, n, seed):
+        def make():
+            return {"a": U.gaussian((batch, m, n), seed=seed)}
+        return make
+
+    def tall_flops(m, n):
+        # Householder R (2 m n^2 - 2 n^3 / 3) and the formation of Q (the same)
+        return 4 * m * n * n - 4 * n ** 3 // 3
+
+    for (tb, tm, tn) in ((8192, 128, 64), (256, 4096, 64)):
+        tname = f"qr{tm}x{tn}"
+        w[tname] = Workload(
+            tname, f"qr_with_mode reduced, {tb} x {tm}x{tn} fp32 N(0,1) (the batched tall QR window)", tb,
+            tall_make(tb, tm, tn, tm + tn), lambda api, t: api.qr(t["a"], "reduced"), "qr_tall",
+            tb * (2 * tm * tn * 4 + tn * tn * 4), tb * tall_flops(tm, tn), "hbm",
+            lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": tb, "rows": tm, "cols": tn})
+
+    # the batched mid-size eigh (65 <= n <= 128, a workgroup of two waves
+    # per matrix): the reference's eigh_ql window past 64
+    def sym_make(batch, n, seed):
+        def make():
+            g = U.gaussian((batch, n, n), seed=seed).astype(np.float64)
+            return {"a": ((g + np.swapaxes(g, -1, -2)) / 2).astype(np.float32)}
+        return make
+
+    w["eigh128"] = Workload(
+        "eigh128", "eigh lower with vectors, 4096 x 128x128 fp32 (G + G^T)/2, G ~ N(0,1) (the batched mid-size "
+                   "eigh window)", 4096, sym_make(4096, 128, 128),
+        lambda api, t: api.eigh(t["a"], True, True), "eigh_mid", 4096 * (2 * 128 * 128 * 4 + 128 * 4 + 4),
+        4096 * (4 * 128 ** 3 // 3 + 2 * 128 ** 3), "hbm",
+        lambda o, h, n: o.eigh(h["a"][:n], True, True), {"batch": 4096, "n": 128})
+
     def chol5_make():
         return {"a": U.config5_spd(U.config5_matrix())}
 

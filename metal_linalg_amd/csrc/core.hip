@@ -131,10 +131,11 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
         return;
     }
     const bool small = eigh_small_fits(n);
-    if (!small && !eigh_blocked_fits(n))
+    const bool mid = eigh_mid_fits(n);
+    if (!small && !mid && !eigh_blocked_fits(n))
         invalid("[eigh] n = " + std::to_string(n) + ": this build's eigh kernels take n <= 16384");
     Call call;
-    if (small) {
+    if (small || mid) {
         // no convergence read-back: bisection always ends (every info word
         // carries bit 16, or bit 17 for a non-finite matrix), so the
         // reference's non-convergence error cannot arise on this path
@@ -142,10 +143,12 @@ void eigh(const Matrices& a, bool lower, float* w, float* v, uint32_t* info) {
                                              {nullptr, w, (size_t)n * 4},
                                              {nullptr, v, v ? (size_t)n * n * 4 : 0},
                                              {nullptr, info, 4}};
-        const size_t wsb = eigh_small_workspace(n, call.chunk_size(B, sl), v != nullptr);
+        const uint32_t chunk = call.chunk_size(B, sl);
+        const size_t wsb = small ? eigh_small_workspace(n, chunk, v != nullptr) : eigh_mid_workspace(n, chunk, v != nullptr);
         float* ws = wsb ? static_cast<float*>(call.scratch(wsb)) : nullptr;
         call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t s) {
-            eigh_small(f32(d[0]), f32(d[1]), f32(d[2]), u32p(d[3]), nb, n, lower, ws, s);
+            if (small) eigh_small(f32(d[0]), f32(d[1]), f32(d[2]), u32p(d[3]), nb, n, lower, ws, s);
+            else eigh_mid(f32(d[0]), f32(d[1]), f32(d[2]), u32p(d[3]), nb, n, lower, ws, s);
         });
         call.finish();
         return;

@@ -73,6 +73,13 @@ size_t eigh_small_workspace(uint32_t n, uint32_t batch, bool vectors);
 void eigh_small(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
                 hipStream_t s);
 
+// ---- symmetric eigendecomposition, 65 <= n <= 128, batched ----
+bool eigh_mid_fits(uint32_t n);
+// Bytes of device workspace eigh_mid needs (0 without vectors).
+size_t eigh_mid_workspace(uint32_t n, uint32_t batch, bool vectors);
+void eigh_mid(const float* a, float* w, float* v, uint32_t* info, uint32_t batch, uint32_t n, bool lower, float* ws,
+              hipStream_t s);
+
 // ---- symmetric eigendecomposition for larger n (<= 16384), one matrix at a time ----
 struct EighWork {
     float *A, *V, *W, *abuf, *y, *partA, *partB, *d, *e, *tau;
