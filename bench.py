@@ -222,6 +222,14 @@ def workloads():
         4096 * (4 * 128 ** 3 // 3 + 2 * 128 ** 3), "hbm",
         lambda o, h, n: o.eigh(h["a"][:n], True, True), {"batch": 4096, "n": 128})
 
+    # the batched mid-size SVD (65 <= min(m, n) <= 128, one-sided Jacobi
+    # in LDS): the reference's golub_kahan window past 64
+    w["svd128"] = Workload(
+        "svd128", "thin SVD with vectors, 4096 x 128x128 fp32 N(0,1) (the batched mid-size SVD window)", 4096,
+        tall_make(4096, 128, 128, 257), lambda api, t: api.svd(t["a"], True), "svd_jacobi",
+        4096 * (3 * 128 * 128 * 4 + 128 * 4 + 4), 4096 * 22 * 128 ** 3, "hbm",
+        lambda o, h, n: o.svd(h["a"][:n], True), {"batch": 4096, "rows": 128, "cols": 128})
+
     def chol5_make():
         return {"a": U.config5_spd(U.config5_matrix())}
 

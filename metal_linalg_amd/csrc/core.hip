@@ -263,6 +263,22 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
         }
         return;
     }
+    if (!svd_small_fits(M, N) && svd_mid_fits(M, N)) {
+        Call call;
+        uint32_t* ibuf = info ? info : call.tmp<uint32_t>(B);
+        const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)M * N * 4},
+                                             {nullptr, u, u ? (size_t)M * K * 4 : 0},
+                                             {nullptr, s, (size_t)K * 4},
+                                             {nullptr, vt, vt ? (size_t)K * N * 4 : 0},
+                                             {nullptr, ibuf, 4}};
+        call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t st) {
+            svd_mid(f32(d[0]), f32(d[1]), f32(d[2]), f32(d[3]), u32p(d[4]), nb, M, N, st);
+        });
+        if (is_device_memory(ibuf)) check_converged(ibuf, B, call.stream(), "svd");
+        else check_converged_host(ibuf, B, "svd");
+        call.finish();
+        return;
+    }
     if (!svd_small_fits(M, N)) {
         if (K <= 64) {
             svd_tall(a, u, s, vt, info);

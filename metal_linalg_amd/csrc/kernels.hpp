@@ -110,6 +110,12 @@ size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes
 void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, float* ws, uint32_t batch, uint32_t m,
                uint32_t n, hipStream_t st);
 
+// ---- thin SVD, 65 <= min(m, n) <= 128 and max(m, n) <= 128, batched ----
+// One-sided Jacobi in LDS; u and vt both or neither; no workspace.
+bool svd_mid_fits(uint32_t m, uint32_t n);
+void svd_mid(const float* a, float* u, float* s, float* vt, uint32_t* info, uint32_t batch, uint32_t m, uint32_t n,
+             hipStream_t st);
+
 // ---- fp32 MFMA GEMM: C = alpha op(A) op(B) + beta C, row-major, strided batches ----
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
            const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
