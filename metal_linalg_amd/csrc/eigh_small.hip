@@ -288,8 +288,23 @@ __device__ __forceinline__ void eigh_vectors(EighLds<N>& s, float (&x)[N], float
     int rounds = pos;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) rounds = max(rounds, __shfl_xor(rounds, off, 64));
+    // inside a group, shifts at least 10 eps |T| apart (sstein's PERTOL):
+    // with equal shifts every member's solve would be drawn to the same
+    // vector of the group, and the Gram-Schmidt rounds would leave noise.
+    // Member t of the group takes max(lam_t, shift_{t-1} + pertol), the
+    // lanes reading the members' values in uniform rounds.
+    float sigma = lam;
+    {
+        const float pertol = 10.0f * kEps * tnorm;
+        float sp = __shfl(lam, g * N + cs, 64);
+        for (int t = 1; t <= rounds; ++t) {
+            const float lt = __shfl(lam, g * N + min(cs + t, N - 1), 64);
+            if (t <= pos) sp = fmaxf(lt, sp + pertol);
+        }
+        if (pos > 0) sigma = sp;
+    }
     for (int pass = 0; pass < (all_diag ? 0 : 2); ++pass) {
-        float a = s.d[0] - lam, cc = s.e[0], b0 = x[0];
+        float a = s.d[0] - sigma, cc = s.e[0], b0 = x[0];
         // d and e of the next row are read one step ahead (their LDS
         // latency hides behind this step's recurrence)
         float enow = s.e[0], dnx = s.d[1], enx = s.e[1];
@@ -297,7 +312,7 @@ __device__ __forceinline__ void eigh_vectors(EighLds<N>& s, float (&x)[N], float
         for (int k = 0; k < N; ++k) {
             if (k + 1 < N) {
                 const float ek = enow;
-                const float an = dnx - lam, cn = enx, b1 = x[k + 1];
+                const float an = dnx - sigma, cn = enx, b1 = x[k + 1];
                 enow = enx;
                 if (k + 2 < N) {
                     dnx = s.d[k + 2];
@@ -337,7 +352,7 @@ __device__ __forceinline__ void eigh_vectors(EighLds<N>& s, float (&x)[N], float
                     enx2 = s.e[k];
                 }
                 const bool swapped = u[k] != u[k];
-                const float q1 = swapped ? (dk1 - lam) * rk : u[k];
+                const float q1 = swapped ? (dk1 - sigma) * rk : u[k];
                 const float q2 = swapped ? ek1 * rk : 0.0f;
                 xv = fmaf(-q2, x2, fmaf(-q1, x1, xv));
             }

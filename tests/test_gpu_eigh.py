@@ -129,3 +129,22 @@ def test_result_does_not_depend_on_batch_position(cuda, api):
     assert np.array_equal(w1.view(np.uint32), w2[::-1].view(np.uint32))
     assert np.array_equal(v1.view(np.uint32), v2[::-1].view(np.uint32))
     assert np.array_equal(i1, i2[::-1])
+
+
+@pytest.mark.parametrize("n", [16, 32, 64])
+def test_large_groups_of_close_eigenvalues(cuda, api, oracle, n):
+    """Half the spectrum one eigenvalue and half another (groups of n / 2
+    for the Gram-Schmidt rounds), and a group spread over 1e-7: the
+    inverse-iteration shifts inside a group are set apart (sstein's rule),
+    so every member converges to its own vector of the group."""
+    rng = np.random.default_rng(n + 1)
+    mats = [with_spectrum(rng, np.repeat([2.0, -1.0], n // 2)),
+            with_spectrum(rng, np.concatenate([1.0 + 1e-7 * np.arange(n // 2), np.linspace(-3, -2, n - n // 2)])),
+            with_spectrum(rng, np.repeat([0.0, 5.0], n // 2))]
+    a = np.stack(mats)
+    w, v, info = api.eigh(a, True, True)
+    wo, _, _ = oracle.eigh(a, True, False)
+    recon, ortho = eigh_residuals(a, w, v)
+    print(f"[eigh groups n={n}] recon {np.array2string(recon, precision=2)} ortho {np.array2string(ortho, precision=2)}")
+    assert recon.max() <= bound(n) and ortho.max() <= bound(n)
+    assert values_close(w, wo).max() <= 1e-5
