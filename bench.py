@@ -44,8 +44,12 @@ FP32_MFMA_PEAK_TFS = 157.3     # MI355X dense fp32 matrix, published
 # x1.9998, WRITE_SIZE x1.0); the runs and the scaling are in
 # profiles/<kernel>_<workload>.md.  Workloads not yet counted report null.
 TRAFFIC_BYTES = {
-    "eigh": 101_633_352 + 111_206_679,  # profiles/eigh_small_eigh.md
-    "qr": 41_840_322 + 81_920_000,     # profiles/qr_small_qr.md
+    "eigh": 212_219_885, # profiles/eigh_small_eigh.md
+    "qr": 123_554_339, # profiles/qr_small_qr.md
+    "qr128x64": 672_378_494, # profiles/qr_tall_qr128x64.md
+    "qr4096x64": 2_627_819_140, # profiles/qr_tall_qr4096x64.md
+    "eigh128": 2_753_827_916, # profiles/eigh_mid_eigh128.md
+    "svd128": 807_681_288, # profiles/svd_jacobi_svd128.md
 }
 
 # The batched kernels are bound by instruction issue, not HBM: VALU
@@ -53,9 +57,12 @@ TRAFFIC_BYTES = {
 # call's kernels; profiles/valu_instructions.md).  A wave64 VALU instruction
 # occupies its SIMD for 4 cycles; MI355X has 1024 SIMDs at 2.4 GHz.
 VALU_INSTRUCTIONS = {
-    "qr": 36_865_000,
-    "eigh": 89_886_238 + 48_865_829,
-    "svd": 93_806_592 + 162_341_627 + 51_152_896,
+    "qr": 24_930_000,
+    "eigh": 138_789_423,
+    "svd": 307_301_115,
+    "qr128x64": 388_014_080,
+    "eigh128": 830_838_762,
+    "svd128": 9_048_489_876,
 }
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
@@ -410,6 +417,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="eigh")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-host-path", action="store_true",
+                    help="skip the host-pointer leg (for profiler runs that count only the device calls)")
     ap.add_argument("--cpu-seconds", type=float, default=2.0, help="wall seconds of the CPU baseline sample")
     args = ap.parse_args()
 
@@ -479,7 +488,7 @@ def main():
                               "frac": round(issue_s / kernel_s_per_call, 4)}
 
     # host-pointer (PCIe-inclusive) rate, for the record; never `value`
-    host_path = host_pointer_path(wl, api, host, max(1, min(5, args.steps)))
+    host_path = None if args.no_host_path else host_pointer_path(wl, api, host, max(1, min(5, args.steps)))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -501,7 +510,7 @@ def main():
         "config": dict({"workload": wl.desc}, **wl.shape),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "host_pointer_rate": host_path["value"],
+        "host_pointer_rate": host_path["value"] if host_path else None,
         "host_pointer": host_path,
         "kernels": {k: {"launches": v[0], "total_ms": round(v[1], 4)} for k, v in other.items()},
         "device": _lib.device_name().decode(),
