@@ -355,18 +355,52 @@ void split_rows_gemm(bool tb, int M, int N, int K, const float* A, int lda, cons
 
 }  // namespace
 
+size_t apply_reflectors_wy_floats(int rows, int cols) {
+    const size_t nsplit = (rows + kRowChunk - 1) / kRowChunk;
+    const size_t wide = std::max(cols, NBT);
+    return nsplit * NBT * wide + 2 * (size_t)NBT * wide + 2 * (size_t)NBT * NBT + 4 * 64;
+}
+
+// Z (rows x cols, row-major) <- H_0 H_1 ... H_{nrefl-1} Z, H_j = I - tau_j v_j
+// v_j^T, v_j stored as row j of V (stride ldv, `rows` entries, zero before
+// its leading 1); panels of NBT reflectors from the last, each in compact WY
+// form: S = V^T V, T from S and tau (wy_t_kernel), Z2 -= V (T (V^T Z2)),
+// the products on the MFMA GEMM.  Rows before the panel's first reflector
+// are zero in all of its reflectors and are left out.
+void apply_reflectors_wy(const float* V, int ldv, const float* tau, int nrefl, int rows, float* Z, int cols,
+                         float* work, hipStream_t s) {
+    if (nrefl <= 0 || cols <= 0) return;
+    const size_t nsplit = (rows + kRowChunk - 1) / kRowChunk;
+    const size_t wide = std::max(cols, NBT);
+    float* part = work;
+    float* Wb = part + nsplit * NBT * wide;
+    float* W2 = Wb + (size_t)NBT * wide;
+    float* Sg = W2 + (size_t)NBT * wide;
+    float* Tg = Sg + (size_t)NBT * NBT;
+    for (int j0 = (nrefl - 1) / NBT * NBT; j0 >= 0; j0 -= NBT) {
+        const int nb = std::min(NBT, nrefl - j0);
+        const int r = rows - j0;
+        const float* Vp = V + (size_t)j0 * ldv + j0;   // reflector k: Vp[k * ldv + i], i = row - j0
+        float* Z2 = Z + (size_t)j0 * cols;
+        split_rows_gemm(true, nb, nb, r, Vp, ldv, Vp, ldv, part, Sg, s);
+        hipLaunchKernelGGL(wy_t_kernel, dim3(1), dim3(64), 0, s, Sg, tau + j0, nb, Tg);
+        split_rows_gemm(false, nb, cols, r, Vp, ldv, Z2, cols, part, Wb, s);
+        sgemm(false, false, nb, cols, nb, 1.0f, Tg, nb, 0, Wb, cols, 0, 0.0f, W2, cols, 0, 1, s);
+        sgemm(true, false, r, cols, nb, -1.0f, Vp, ldv, 0, W2, cols, 0, 1.0f, Z2, cols, 0, 1, s);
+    }
+}
+
 size_t eigh_tridiag_floats(uint32_t n) {
     const size_t N = n;
     // lam, e2, slots/clusters (as floats), perm; Z; scratch (G, inverse
     // iteration's factor: 3 N per cluster); the back-transform's partials
-    const size_t nsplit = (N + kRowChunk - 1) / kRowChunk;
-    return 4 * N + 12 * N + N * N + N + 3 * N * N + nsplit * NBT * N + 2 * (size_t)NBT * N + 2 * (size_t)NBT * NBT +
-           64 * 16;
+    return 4 * N + 12 * N + N * N + N + 3 * N * N + apply_reflectors_wy_floats((int)N, (int)N) + 64 * 16;
 }
 
 // Stages 2 and 3 on one matrix after sytrd_one: w_out (n), and if v_out
 // V (n x n) with the eigenvectors as columns; info.
-void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out, uint32_t* info, hipStream_t s) {
+void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out, uint32_t* info, hipStream_t s,
+                      bool backtransform) {
     const int n = (int)nn;
     const size_t N = nn;
     float* p = w.rest;
@@ -383,12 +417,7 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
     float* Z = take(N * N);
     float* dE = take(N);                 // e with the splits zeroed
     float* scratch = take(3 * N * N);    // inverse iteration's factor, then Z^T Z
-    const size_t nsplit = (N + kRowChunk - 1) / kRowChunk;
-    float* part = take(nsplit * NBT * N);
-    float* Wb = take((size_t)NBT * N);
-    float* W2 = take((size_t)NBT * N);
-    float* Sg = take((size_t)NBT * NBT);
-    float* Tg = take((size_t)NBT * NBT);
+    float* part = take(apply_reflectors_wy_floats(n, n));   // the back-transform's products
 
     hipLaunchKernelGGL(set_info_kernel, dim3(1), dim3(1), 0, s, info, w.flags);
     // the small host-side bookkeeping: T's entries, the splits and Gershgorin
@@ -491,23 +520,11 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
         tm.stop();
     }
     // V = Q Z: panels from the last, Z2 = Z[j0 + 1 :, :] -= V (T (V^T Z2))
-    {
+    // (row j0 is zero in every reflector of the panel, kept so that the
+    // operands stay 16-byte aligned)
+    if (backtransform) {
         KernelTimer tm("eigh_backtransform", s);
-        const int nrefl = n - 1;
-        for (int j0 = (nrefl - 1) / NBT * NBT; j0 >= 0; j0 -= NBT) {
-            const int nb = std::min(NBT, nrefl - j0);
-            // rows j0 .. n-1 (row j0 is zero in every reflector of the panel,
-            // kept so that the operands stay 16-byte aligned)
-            const int rows = n - j0;
-            const float* Vp = w.V + (size_t)j0 * N + j0;   // reflector k: Vp[k * N + r], r = row - j0
-            float* Z2 = Z + (size_t)j0 * N;
-            // S = V^T V, T
-            split_rows_gemm(true, nb, nb, rows, Vp, n, Vp, n, part, Sg, s);
-            hipLaunchKernelGGL(wy_t_kernel, dim3(1), dim3(64), 0, s, Sg, w.tau + j0, nb, Tg);
-            split_rows_gemm(false, nb, n, rows, Vp, n, Z2, n, part, Wb, s);
-            sgemm(false, false, nb, n, nb, 1.0f, Tg, nb, 0, Wb, n, 0, 0.0f, W2, n, 0, 1, s);
-            sgemm(true, false, rows, n, nb, -1.0f, Vp, n, 0, W2, n, 0, 1.0f, Z2, n, 0, 1, s);
-        }
+        apply_reflectors_wy(w.V, n, w.tau, n - 1, n, Z, n, part, s);
         tm.stop();
     }
     hipLaunchKernelGGL(permute_columns_kernel, dim3((unsigned)cdiv(N * N, 256)), dim3(256), 0, s, Z, v_out, perm, n);

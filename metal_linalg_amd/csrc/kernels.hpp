@@ -95,16 +95,40 @@ void eigh_unscale(const float* x, float* y, uint32_t count, const uint32_t* flag
 // stages 2 and 3 after sytrd_one: eigenvalues (ascending), eigenvectors if
 // v_out, info; the workspace after stage 1's holds eigh_tridiag_floats(n)
 size_t eigh_tridiag_floats(uint32_t n);
-void eigh_tridiag_one(const EighWork& w, uint32_t n, float* w_out, float* v_out, uint32_t* info, hipStream_t s);
+void eigh_tridiag_one(const EighWork& w, uint32_t n, float* w_out, float* v_out, uint32_t* info, hipStream_t s,
+                      bool backtransform = true);
+// Z (rows x cols, row-major) <- H_0 H_1 ... H_{nrefl-1} Z with H_j = I -
+// tau_j v_j v_j^T, v_j row j of V (stride ldv, zero before its leading 1),
+// in compact-WY panels on the MFMA GEMM; work = apply_reflectors_wy_floats.
+size_t apply_reflectors_wy_floats(int rows, int cols);
+void apply_reflectors_wy(const float* V, int ldv, const float* tau, int nrefl, int rows, float* Z, int cols,
+                         float* work, hipStream_t s);
 
-// ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128 ----
-// One m x n matrix with min(m, n) > 64 (max(m, n) <= 4096), through the
-// large eigh path on [0 A^T; A 0]; work = svd_large_workspace(m, n) bytes.
+// Golub-Kahan bidiagonalisation of one tall matrix (m x k, m >= k), for the
+// large SVD: T = Q B P^T, B upper bidiagonal (d, e), the reflectors of Q as
+// the rows of VL (leading 1 at j) with tauq, those of P as the rows of VR
+// (leading 1 at j + 1) with taup; B is T's scaled by 2^-e (flags[0] = bits
+// of max |T|, flags[1] = a non-finite entry, which zeroes the work).
+struct Bidiag {
+    float *Ac, *VL, *VR, *tauq, *taup, *d, *e, *x, *rowbuf;
+    uint32_t* flags;
+};
+size_t bidiag_floats(uint32_t m, uint32_t k);
+Bidiag bidiag_carve(float* base, uint32_t m, uint32_t k);
+void bidiag_one(const float* T, uint32_t m, uint32_t k, const Bidiag& b, hipStream_t s);
+// the Golub-Kahan tridiagonal of B (2k x 2k, zero diagonal td, off-diagonal
+// te = d_0, e_0, d_1, ..., d_{k-1})
+void tgk_build(const Bidiag& b, uint32_t k, float* td, float* te, hipStream_t s);
+
+// One m x n matrix beyond the batched windows (max(m, n) <= 4096):
+// bidiagonalisation, the Golub-Kahan tridiagonal's eigenpairs, the
+// reflectors' back-transforms; work = svd_large_workspace(m, n) bytes.
 bool svd_large_fits(uint32_t m, uint32_t n);
 size_t svd_large_workspace(uint32_t m, uint32_t n);
 void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info, float* work, uint32_t m,
                    uint32_t n, hipStream_t st);
 
+// ---- thin SVD, min(m, n) <= 64, max(m, n) <= 128, batched ----
 bool svd_small_fits(uint32_t m, uint32_t n);
 size_t svd_small_workspace(uint32_t m, uint32_t n, uint32_t batch);   // bytes
 void svd_small(const float* a, float* u, float* s, float* vt, uint32_t* info, float* ws, uint32_t batch, uint32_t m,

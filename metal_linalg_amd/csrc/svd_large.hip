@@ -1,5 +1,6 @@
-// Thin SVD of a single larger matrix (min(M, N) > 64, max(M, N) <= 4096),
-// through the symmetric eigensolver of this build.
+// Thin SVD of a single larger matrix (beyond the batched windows, max(M, N)
+// <= 4096), by bidiagonalisation and the symmetric tridiagonal eigensolver of
+// this build.
 //
 // Role: the MI355X counterpart of the reference's large-matrix SVD routes
 // (reference: src/svd.mm:902-1026 routing, src/svd_bidiag.mm for the band /
@@ -10,16 +11,19 @@
 // FLT_EPSILON s_max (the batched kernels' rank-deficient rule).
 //
 // Method: the tall problem T (m x k, m >= k; a wide A is solved as A^T) is
-// embedded in the symmetric (m + k) x (m + k) matrix H = [0 T^T; T 0], whose
-// eigenvalues are +-s_i and m - k zeros, with eigenvectors (v_i; u_i) / sqrt 2
-// for +s_i (Jordan-Wielandt).  H goes through the blocked tridiagonalisation,
-// bisection and inverse iteration of the large eigh path; the k largest
-// eigenpairs give s, U and V.  Where the smallest s_i come within the
-// solver's grouping distance of zero, +-s_i and the zeros form one close
+// bidiagonalised, T = Q B P^T (svd_bidiag.hip).  B's singular triplets are
+// the eigenpairs of its Golub-Kahan tridiagonal (2k x 2k, zero diagonal,
+// off-diagonal d_0, e_0, d_1, ...): eigenvalues +-s_i, eigenvectors
+// (v_1, u_1, v_2, u_2, ...) / sqrt 2 for +s_i, computed by the large eigh
+// path's bisection and inverse iteration.  U = Q U_B and V = P V_B by the
+// reflectors in compact-WY panels on the MFMA GEMM.  Where the smallest s_i
+// come within the solver's grouping distance of zero, +-s_i form one close
 // group, in which the solver returns some orthonormal basis of the invariant
 // subspace: the u and v parts of those columns are not singular vectors.
 // They are rebuilt (see svd_large_one): orthonormal completions of the
-// well-separated columns, rotated by a small SVD (Rayleigh-Ritz).
+// well-separated columns, rotated by a small SVD (Rayleigh-Ritz).  The
+// earlier route embedded T in the (m + k)-square Jordan-Wielandt matrix
+// and tridiagonalised that: eight times the reduction's work at m = k.
 #include <algorithm>
 #include <cmath>
 #include <vector>
@@ -31,44 +35,33 @@
 namespace mla {
 namespace {
 
-// H = [0 T^T; T 0] (n2 = k + m), T row-major m x k
-__global__ __launch_bounds__(256) void jw_build_kernel(const float* __restrict__ T, int m, int k,
-                                                       float* __restrict__ H) {
-    const int n2 = m + k;
+// From the Golub-Kahan tridiagonal's eigenpairs (ascending w, Z 2k x 2k):
+// s_i = max(w[2k-1-i], 0) (NaN kept); U[r][i] = sqrt2 Z[2r+1][2k-1-i] for r < k (rows
+// k .. m-1 of U zero: Q's reflectors fill them); V[c][i] (as Vt[i][c]) =
+// sqrt2 Z[2c][2k-1-i]
+__global__ __launch_bounds__(256) void tgk_extract_kernel(const float* __restrict__ Z, const float* __restrict__ w,
+                                                          int m, int k, float* __restrict__ U, float* __restrict__ Vt,
+                                                          float* __restrict__ s) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)n2 * n2) return;
-    const int i = (int)(idx / n2), j = (int)(idx - (size_t)i * n2);
-    float v = 0.0f;
-    if (i >= k && j < k) v = T[(size_t)(i - k) * k + j];
-    else if (i < k && j >= k) v = T[(size_t)(j - k) * k + i];
-    H[idx] = v;
-}
-
-// s_i = max(w[n2-1-i], 0); U[r][i] = sqrt2 Z[k + r][n2-1-i]; V[c][i] (as
-// Vt[i][c]) = sqrt2 Z[c][n2-1-i]
-__global__ __launch_bounds__(256) void jw_extract_kernel(const float* __restrict__ Z, const float* __restrict__ w,
-                                                         int m, int k, float* __restrict__ U, float* __restrict__ Vt,
-                                                         float* __restrict__ s) {
-    const int n2 = m + k;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const float r2 = 1.41421356237309515f;
+    const int n2 = 2 * k;
+    const float sq2 = 1.41421356237f;
     if (idx < (size_t)k) {
-        const float x = w[n2 - 1 - (int)idx];
-        s[idx] = x != x ? x : fmaxf(x, 0.0f);   // NaN stays NaN
+        const float x = w[n2 - 1 - idx];
+        s[idx] = x != x ? x : fmaxf(x, 0.0f);   // a NaN (non-finite input) stays NaN
     }
-    if (!U) return;
-    if (idx < (size_t)m * k) {
+    if (Z == nullptr) return;
+    if (U && idx < (size_t)m * k) {
         const int r = (int)(idx / k), i = (int)(idx - (size_t)r * k);
-        U[idx] = r2 * Z[(size_t)(k + r) * n2 + (n2 - 1 - i)];
+        U[idx] = r < k ? sq2 * Z[(size_t)(2 * r + 1) * n2 + (n2 - 1 - i)] : 0.0f;
     }
     if (idx < (size_t)k * k) {
         const int i = (int)(idx / k), c = (int)(idx - (size_t)i * k);
-        Vt[idx] = r2 * Z[(size_t)c * n2 + (n2 - 1 - i)];
+        Vt[idx] = sq2 * Z[(size_t)(2 * c) * n2 + (n2 - 1 - i)];
     }
 }
 
 // Each column of X (rows x cols, row-major) scaled to unit length: an
-// eigenvector of H can carry a little of its -s partner, which moves weight
+// eigenvector of the tridiagonal can carry a little of its -s partner, which moves weight
 // between its u and v parts without turning either.  One thread per column;
 // the loop walks rows, so a wave reads consecutive columns of one row.
 __global__ __launch_bounds__(256) void normalize_cols_kernel(float* __restrict__ X, int rows, int cols) {
@@ -118,23 +111,24 @@ void copy_block(const float* src, int lds, float* dst, int ldd, int rows, int co
 
 bool svd_large_fits(uint32_t m, uint32_t n) {
     const uint32_t l = std::max(m, n), k = std::min(m, n);
-    return k >= 1 && qr_blocked_fits(l, k) && eigh_blocked_fits(l + k);
+    return k >= 1 && qr_blocked_fits(l, k) && eigh_blocked_fits(2 * k);
 }
 
 size_t svd_large_workspace(uint32_t m, uint32_t n) {
-    const size_t l = std::max(m, n), k = std::min(m, n), n2 = l + k;
-    size_t floats = eigh_sytrd_floats((uint32_t)n2) + eigh_tridiag_floats((uint32_t)n2);
-    floats += 2 * n2 * n2 + n2 + 64;            // H, Z, w
+    const size_t l = std::max(m, n), k = std::min(m, n), n2 = 2 * k;
+    size_t floats = bidiag_floats((uint32_t)l, (uint32_t)k) + eigh_tridiag_floats((uint32_t)n2);
+    floats += 2 * n2 + n2 * n2 + n2 + 64;            // the tridiagonal, Z, w
     floats += 4 * l * k + 3 * k * k + 3 * 64 * 64;   // T, U, Q, C, V, Vt', R
     floats += svd_small_workspace(64, 64, 1) / sizeof(float) + 64;
+    floats += apply_reflectors_wy_floats((int)l, (int)k) + 64;
     const size_t qw = qr_blocked_workspace((uint32_t)l, (uint32_t)k) / sizeof(float) + 64;
-    return (floats + qw + 16 * 64) * sizeof(float);   // + the 64-float rounding of each piece
+    return (floats + qw + 20 * 64) * sizeof(float);   // + the 64-float rounding of each piece
 }
 
 void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info, float* work, uint32_t M,
                    uint32_t N, hipStream_t st) {
     const bool wide = M < N;
-    const int m = (int)(wide ? N : M), k = (int)(wide ? M : N), n2 = m + k;
+    const int m = (int)(wide ? N : M), k = (int)(wide ? M : N), n2 = 2 * k;
     const bool vec = u != nullptr;
     float* p = work;
     auto take = [&](size_t floats) {
@@ -142,9 +136,12 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
         p += (floats + 63) / 64 * 64;
         return q;
     };
-    const EighWork ew = eigh_carve(take(eigh_sytrd_floats((uint32_t)n2) + eigh_tridiag_floats((uint32_t)n2)),
-                                   (uint32_t)n2);
-    float* H = take((size_t)n2 * n2);
+    const Bidiag bd = bidiag_carve(take(bidiag_floats((uint32_t)m, (uint32_t)k)), (uint32_t)m, (uint32_t)k);
+    EighWork ew{};
+    ew.d = take((size_t)n2);
+    ew.e = take((size_t)n2);
+    ew.flags = bd.flags;
+    ew.rest = take(eigh_tridiag_floats((uint32_t)n2));
     float* Z = vec ? take((size_t)n2 * n2) : nullptr;
     float* w = take((size_t)n2);
     float* T = take((size_t)m * k);
@@ -155,6 +152,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     float* R = take((size_t)k * k + 3 * 64 * 64);
     float* C = take((size_t)m * k);
     float* sws = take(svd_small_workspace(64, 64, 1) / sizeof(float) + 64);
+    float* wyw = take(apply_reflectors_wy_floats(m, k));
     float* qw = take(qr_blocked_workspace((uint32_t)m, (uint32_t)k) / sizeof(float) + 64);
     uint32_t* dinfo = reinterpret_cast<uint32_t*>(take(64));
 
@@ -163,16 +161,20 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
         transpose_full(a, T, (int)M, (int)N, st);
         tall = T;
     }
-    hipLaunchKernelGGL(jw_build_kernel, dim3(blocks((size_t)n2 * n2)), dim3(256), 0, st, tall, m, k, H);
-    sytrd_one(H, (uint32_t)n2, true, ew, st);
-    eigh_tridiag_one(ew, (uint32_t)n2, w, Z, dinfo, st);
-    hipLaunchKernelGGL(jw_extract_kernel, dim3(blocks(std::max((size_t)m * k, (size_t)k * k))), dim3(256), 0, st, Z,
+    bidiag_one(tall, (uint32_t)m, (uint32_t)k, bd, st);
+    tgk_build(bd, (uint32_t)k, ew.d, ew.e, st);
+    eigh_tridiag_one(ew, (uint32_t)n2, w, Z, dinfo, st, false);
+    hipLaunchKernelGGL(tgk_extract_kernel, dim3(blocks(std::max((size_t)m * k, (size_t)k * k))), dim3(256), 0, st, Z,
                        w, m, k, vec ? Ut : nullptr, Vtt, s);
 
     if (vec) {
+        // B's vectors to unit length (an eigenvector of the tridiagonal can
+        // carry a little of its -s partner), then U = Q U_B, V = P V_B
         hipLaunchKernelGGL(normalize_cols_kernel, dim3(blocks((size_t)k)), dim3(256), 0, st, Ut, m, k);
         transpose_full(Vtt, V, k, k, st);
         hipLaunchKernelGGL(normalize_cols_kernel, dim3(blocks((size_t)k)), dim3(256), 0, st, V, k, k);
+        apply_reflectors_wy(bd.VL, m, bd.tauq, k, m, Ut, k, wyw, st);
+        apply_reflectors_wy(bd.VR, k, bd.taup, k - 1, k, V, k, wyw, st);
     }
     // the host decides: non-finite input, the rank rule, the completion
     uint32_t hinfo = 0;
@@ -185,8 +187,8 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     if (!bad) {
         const float smax = hs[0], smin = hs[(size_t)k - 1];
         out_info = 1u | (1u << 16) | (!(smin > 32.0f * FLT_EPSILON * smax) ? (1u << 18) : 0u);
-        // The close group around zero: -s_i, the m - k zeros and +s_i share
-        // one group in the eigensolver (which returns some orthonormal basis
+        // The close group around zero: -s_i and +s_i share one group in the
+        // eigensolver (which returns some orthonormal basis
         // of it) from the smallest s upwards while the gaps stay below the
         // solver's grouping distance (taken generously, 4e-5 s_max).  Those
         // columns, J = g .. k-1, are rebuilt: V_J and U_J as the orthonormal
@@ -196,7 +198,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
         // gives their singular values.
         const float thr = 4e-5f * smax;
         int g = k;
-        if (((m > k) ? hs[(size_t)k - 1] : 2.0f * hs[(size_t)k - 1]) <= thr) {
+        if (2.0f * hs[(size_t)k - 1] <= thr) {
             g = k - 1;
             while (g > 0 && hs[(size_t)g - 1] - hs[(size_t)g] <= thr) --g;
         }
