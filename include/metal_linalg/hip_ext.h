@@ -46,6 +46,16 @@ int metal_linalg_hip_sgemm(int transa, int transb, int M, int N, int K, float al
  * metal_linalg_status value.  For tests. */
 int metal_linalg_hip_sytrd(const float* a, uint32_t n, int lower, float* d, float* e);
 
+/* Orders the library's next calls after the work enqueued so far on
+ * `stream` (a hipStream_t of the library's device, as void*; NULL is the null
+ * stream) without blocking the host: an event recorded on `stream` that the
+ * library's own stream waits for.  No counterpart in the reference, whose
+ * calls take no stream: it is for frameworks whose kernels produce the
+ * inputs on a stream of their own (the PyTorch binding calls it before every
+ * operation on ROCm tensors).  The library's calls still return only when
+ * their results are complete.  Returns a metal_linalg_status value. */
+metal_linalg_status metal_linalg_hip_stream_wait(void* stream);
+
 /* The device's gcnArchName ("" without a GPU). */
 const char* metal_linalg_hip_arch(void);
 

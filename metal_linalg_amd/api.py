@@ -74,6 +74,19 @@ class _Arrays:
         self.keep.append(x)
         return x
 
+    def call(self, fn, *args):
+        """fn(*args) under the library lock.  For tensors on the GPU the
+        library's stream first waits for what torch has enqueued on its
+        current stream so far, this call's input conversions and output
+        allocations included: an event, not a host synchronisation.  The
+        library returns when its results are complete."""
+        with _lib.lock:
+            if self.torch and self.device.type == "cuda":
+                import torch
+
+                _check(_lib.hip_stream_wait(torch.cuda.current_stream(self.device).cuda_stream))
+            _check(fn(*args))
+
     @staticmethod
     def ptr(x):
         if x is None:
@@ -114,8 +127,7 @@ def qr(a, mode: str = "reduced"):
     rr = m if code == 2 else k
     q = arr.empty(lead + (m, qc)) if qc else None
     r = arr.empty(lead + (rr, n))
-    with _lib.lock:
-        _check(_lib.qr_with_mode(arr.ptr(arr.a), b, m, n, code, arr.ptr(q), arr.ptr(r)))
+    arr.call(_lib.qr_with_mode, arr.ptr(arr.a), b, m, n, code, arr.ptr(q), arr.ptr(r))
     return q, r
 
 
@@ -128,8 +140,7 @@ def eigh(a, lower: bool = True, vectors: bool = True):
     w = arr.empty(lead + (n,))
     v = arr.empty(lead + (n, n)) if vectors else None
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.eigh(arr.ptr(arr.a), b, n, int(bool(lower)), arr.ptr(w), arr.ptr(v), arr.ptr(info)))
+    arr.call(_lib.eigh, arr.ptr(arr.a), b, n, int(bool(lower)), arr.ptr(w), arr.ptr(v), arr.ptr(info))
     return w, v, info
 
 
@@ -142,8 +153,7 @@ def svd(a, vectors: bool = True):
     u = arr.empty(lead + (m, k)) if vectors else None
     vt = arr.empty(lead + (k, n)) if vectors else None
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.svd(arr.ptr(arr.a), b, m, n, arr.ptr(u), arr.ptr(s), arr.ptr(vt), arr.ptr(info)))
+    arr.call(_lib.svd, arr.ptr(arr.a), b, m, n, arr.ptr(u), arr.ptr(s), arr.ptr(vt), arr.ptr(info))
     return u, s, vt, info
 
 
@@ -153,8 +163,7 @@ def cholesky(a, upper: bool = False):
     lead, b, n, _ = _dims(arr.a)
     l = arr.empty(lead + (n, n))
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.cholesky(arr.ptr(arr.a), b, n, int(bool(upper)), arr.ptr(l), arr.ptr(info)))
+    arr.call(_lib.cholesky, arr.ptr(arr.a), b, n, int(bool(upper)), arr.ptr(l), arr.ptr(info))
     return l, info
 
 
@@ -165,8 +174,7 @@ def lu_factor(a):
     lu = arr.empty(lead + (n, n))
     piv = arr.empty(lead + (n,), "u32")
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.lu_factor(arr.ptr(arr.a), b, n, arr.ptr(lu), arr.ptr(piv), arr.ptr(info)))
+    arr.call(_lib.lu_factor, arr.ptr(arr.a), b, n, arr.ptr(lu), arr.ptr(piv), arr.ptr(info))
     return lu, piv, info
 
 
@@ -178,8 +186,7 @@ def solve(a, rhs):
     nrhs = int(rhs.shape[-1])
     x = arr.empty(tuple(rhs.shape))
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.solve(arr.ptr(arr.a), b, n, arr.ptr(rhs), nrhs, arr.ptr(x), arr.ptr(info)))
+    arr.call(_lib.solve, arr.ptr(arr.a), b, n, arr.ptr(rhs), nrhs, arr.ptr(x), arr.ptr(info))
     return x, info
 
 
@@ -189,8 +196,7 @@ def inv(a):
     lead, b, n, _ = _dims(arr.a)
     x = arr.empty(lead + (n, n))
     info = arr.empty(lead, "u32")
-    with _lib.lock:
-        _check(_lib.inv(arr.ptr(arr.a), b, n, arr.ptr(x), arr.ptr(info)))
+    arr.call(_lib.inv, arr.ptr(arr.a), b, n, arr.ptr(x), arr.ptr(info))
     return x, info
 
 
@@ -200,9 +206,8 @@ def solve_triangular(a, rhs, upper: bool = False, unit: bool = False):
     rhs = arr.like(rhs)
     nrhs = int(rhs.shape[-1])
     x = arr.empty(tuple(rhs.shape))
-    with _lib.lock:
-        _check(_lib.solve_triangular(arr.ptr(arr.a), b, n, arr.ptr(rhs), nrhs, int(bool(upper)), int(bool(unit)),
-                                     arr.ptr(x)))
+    arr.call(_lib.solve_triangular, arr.ptr(arr.a), b, n, arr.ptr(rhs), nrhs, int(bool(upper)), int(bool(unit)),
+             arr.ptr(x))
     return x
 
 

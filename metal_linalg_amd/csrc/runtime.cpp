@@ -545,6 +545,18 @@ const char* metal_linalg_hip_kernel_names(void) {
     return s.c_str();
 }
 
+metal_linalg_status metal_linalg_hip_stream_wait(void* stream) {
+    return mla::run_entry([&] {
+        std::lock_guard<std::mutex> lock(mla::g_call_mutex);
+        mla::Device& d = mla::device();
+        MLA_HIP(hipSetDevice(d.id));
+        static hipEvent_t ev = nullptr;   // re-recorded each time; a wait takes the record current when made
+        if (!ev) MLA_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        MLA_HIP(hipEventRecord(ev, static_cast<hipStream_t>(stream)));
+        MLA_HIP(hipStreamWaitEvent(d.stream, ev, 0));
+    });
+}
+
 const char* metal_linalg_hip_arch(void) {
     static std::string s;
     s = mla::have_device() ? mla::device().arch : std::string();

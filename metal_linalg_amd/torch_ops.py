@@ -6,9 +6,9 @@ names, arguments and outputs (qr, eigh, eigvalsh, svd, svdvals, cholesky,
 lu_factor, solve, inv, solve_triangular), over this build's C ABI.
 
 A GPU tensor (ROCm: device type "cuda") is read and written in place by the
-library on its own stream; the call first waits for torch's current stream,
-whose queued work may still be writing the input, and returns when the
-results are complete.  A CPU tensor goes through the C ABI's host-pointer
+library on its own stream, which first waits (through an event, without
+blocking the host) for the work queued on torch's current stream, as that may
+still be writing the input; the call returns when the results are complete.  A CPU tensor goes through the C ABI's host-pointer
 path (staged through device memory), so CPU tensors work too, computed on the
 GPU.  Every operator has a fake (meta) implementation giving torch.compile the
 output shapes, and the differentiable ones carry the backward formulas below
@@ -30,13 +30,6 @@ from . import api
 __all__ = ["qr", "eigh", "eigvalsh", "svd", "svdvals", "cholesky", "lu_factor", "solve", "inv", "solve_triangular"]
 
 
-def _wait(*ts):
-    for t in ts:
-        if t.device.type == "cuda":
-            torch.cuda.current_stream(t.device).synchronize()
-            return
-
-
 def _f32(a: Tensor) -> Tensor:
     return a.detach().to(torch.float32).contiguous()
 
@@ -54,8 +47,8 @@ def _back(x, like: Tensor) -> Tensor:
 
 
 def _run(fn, a: Tensor, *rest):
-    """fn over device tensors in place, or over host arrays for CPU tensors."""
-    _wait(a, *rest)
+    """fn over device tensors in place (api orders the library's stream after
+    torch's current one), or over host arrays for CPU tensors."""
     if a.device.type == "cuda":
         return fn(a, *rest)
     return fn(a.numpy(), *[r.numpy() for r in rest])

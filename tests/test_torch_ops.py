@@ -84,6 +84,32 @@ def test_forward_matches_c_abi(cuda):
 
 
 @pytest.mark.gpu
+def test_orders_after_torch_stream(cuda):
+    """The input is still being written by work queued on torch's current
+    stream (a chain of 4096^3 products, milliseconds each) when the operator
+    is called: the library's stream waits for it through an event, and the
+    results equal those on the settled input, bit for bit."""
+    base = torch.tensor(_rand((256, 64, 64), 5), dtype=torch.float32, device="cuda")
+    sym = (base + base.mT).contiguous()
+    ref_w, ref_v, _ = api.eigh(sym)
+    ref_q, ref_r = api.qr(base)
+    torch.cuda.synchronize()
+    for op in ("eigh", "qr"):
+        big = torch.randn(4096, 4096, device="cuda")
+        for _ in range(8):
+            big = (big @ big) * (1.0 / 64)
+        zero = torch.nan_to_num(big[0, 0], nan=0.0, posinf=0.0, neginf=0.0) * 0.0
+        a = torch.zeros_like(base)
+        a.copy_((sym if op == "eigh" else base) + zero)   # written only after the chain
+        if op == "eigh":
+            w, v = ops.eigh(a)
+            assert torch.equal(w, ref_w) and torch.equal(v, ref_v)
+        else:
+            q, r = ops.qr(a)
+            assert torch.equal(q, ref_q) and torch.equal(r, ref_r)
+
+
+@pytest.mark.gpu
 def test_gradients(cuda):
     x = _rand((3, 9, 6), 2)
     sq = lambda t: t * t   # sign-invariant functions of vectors
