@@ -293,6 +293,21 @@ def workloads():
         "qr4096", "qr_with_mode reduced, one 4096x4096 fp32 G ~ N(0,1) (BASELINE config 5)", 1, qr5_make,
         lambda api, t: api.qr(t["a"], "reduced"), "gemm_mfma", None, qr_gemm_flops(n5), "mfma",
         lambda o, h, n: o.qr(h["a"][None], "reduced"), {"n": n5}, unit="GFLOP/s", nominal_flops=8 * n5 ** 3 / 3)
+
+    def bidiag_bytes(m, k):
+        # the one-stage bidiagonalisation's HBM floor: per column the
+        # trailing block is read and written by the left update and read
+        # again by the product A v (it outgrows on-chip memory), 4 B each
+        return sum(4 * (2 * (m - j) * (k - j) + (m - j - 1) * (k - j - 1)) for j in range(k))
+
+    # the large single-matrix SVD (not a BASELINE config): rate by the
+    # nominal count of bidiagonalisation (8/3 n^3) and the two reflector
+    # back-transforms (2 n^3 each), as LAPACK's sgebrd + sormbr
+    w["svd4096"] = Workload(
+        "svd4096", "thin SVD with vectors, one 4096x4096 fp32 G ~ N(0,1) (the large single-matrix SVD)", 1,
+        qr5_make, lambda api, t: api.svd(t["a"], True), "svd_bidiag_large", bidiag_bytes(n5, n5), None, "hbm",
+        lambda o, h, n: o.svd(h["a"][None], True), {"n": n5}, unit="GFLOP/s",
+        nominal_flops=8 * n5 ** 3 // 3 + 4 * n5 ** 3)
     return w
 
 
