@@ -10,7 +10,7 @@
 // triangle of the output is zero.
 //
 // Per panel j (columns j .. j+nb):
-//   chol_diag    one workgroup: the nb x nb diagonal block in LDS, factored,
+//   chol_diag    one 1024-thread workgroup: the nb x nb diagonal block in LDS, factored,
 //                and its triangular inverse X = L11^-1 (forward substitution
 //                on the identity, rows in parallel)
 //   TRSM         L21 = A21 X^T as one MFMA GEMM, in place (one column tile
@@ -52,25 +52,28 @@ __global__ __launch_bounds__(256) void copy_transpose_kernel(const float* __rest
     }
 }
 
-// One workgroup factors the nb x nb diagonal block (nb <= 128, padded to 128
-// with the identity) in LDS and forms the inverse X = L^-1 of its factor, in
-// four sub-panels of 32 columns (right-looking within the block):
+// One workgroup of 1024 threads factors the nb x nb diagonal block (nb <=
+// 128, padded to 128 with the identity) in LDS and forms the inverse X = L^-1
+// of its factor, in four sub-panels of 32 columns (right-looking within the
+// block):
 //   1. wave 0 factors the 32 x 32 diagonal sub-block, lane r holding row r:
 //      per column k the pivot and the scaled column are read across lanes
 //      (readlane, so no LDS round trip or barrier per column), and the same
 //      column values drive, in lanes 32..63, the forward substitution that
 //      builds the sub-block's inverse Y (lane 32 + c holding column c);
-//   2. the rows below, within the block: L = A Y^T (all threads);
-//   3. the trailing lower triangle of the block: A -= L L^T (4 x 4 tiles);
+//   2. the rows below, within the block: L = A Y^T;
+//   3. the trailing lower triangle of the block: A -= L L^T;
 // then the off-diagonal 32 x 32 blocks of X, by block forward substitution:
-// X_ip = -Y_i sum_{k=p}^{i-1} L_ik X_kp, in rounds of i - p = 1, 2, 3.
-// Barriers: a handful per sub-panel instead of one per column.
+// X_ip = -Y_i sum_{k=p}^{i-1} L_ik X_kp, in rounds of i - p = 1, 2, 3.  The
+// products of 2, 3 and the rounds run on the matrix cores, a wave per 32 x 32
+// block (4 x 4 VALU tiles read LDS with 4-way bank conflicts: the trailing
+// update alone took 10 us); the load and store use all sixteen waves.
 //
 // The first pivot that is not positive and finite sets info = j0 + k + 1
 // (unless an earlier block already set it); the factorisation carries on with
 // NaN, which the final extract turns into the all-NaN output.
 constexpr int SB = 32;           // sub-panel width
-constexpr int DT = 256;          // threads of the diagonal-block kernel
+constexpr int DT = 1024;         // threads of the diagonal-block kernel
 constexpr int LDA = NB + 4;      // LDS row stride: rows 16-byte aligned
 
 struct DiagLds {
@@ -80,53 +83,65 @@ struct DiagLds {
     int fail;
 };
 
-// acc (4 x 4) += P[r0 .. r0+3][0 .. 31] Q[0 .. 31][c0 .. c0+3]: P and Q are
-// 32 x 32 blocks with row strides ldp and ldq.
-__device__ __forceinline__ void tile_mm(float (&acc)[4][4], const float* P, int ldp, const float* Q, int ldq, int r0,
-                                        int c0) {
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// acc (a 32 x 32 MFMA block: lane l holds column l % 32, rows 8 (e / 4) +
+// 4 (l / 32) + e % 4) += P Q over K = 16 kt, P = rows of `prow` (32 rows,
+// k contiguous, stride LDA) and Q given either as rows of `qcol` with k
+// contiguous (QKM false: Q[k][c] = qcol[c LDA + k]) or k-major (QKM true:
+// Q[k][c] = qcol[k ldq + c]).  As in the GEMM kernel, lanes 0-31 supply k
+// = 0..7 and lanes 32-63 k = 8..15 of each 16-k step (16-byte P reads).
+template <bool QKM>
+__device__ __forceinline__ void mfma_block(floatx16& acc, const float* prow, const float* qcol, int ldq, int kt,
+                                           int lane) {
+    const int lr = lane & 31, kh = (lane >> 5) * 8;
+    for (int t16 = 0; t16 < kt; ++t16) {
+        const int k = t16 * 16 + kh;
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(prow + lr * LDA + k);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(prow + lr * LDA + k + 4);
+        float b[8];
+        if (QKM) {
 #pragma unroll
-    for (int q0 = 0; q0 < SB; q0 += 4) {
-        float pr[4][4];
+            for (int s = 0; s < 8; ++s) b[s] = qcol[(k + s) * ldq + lr];
+        } else {
+            const floatx4 b0 = *reinterpret_cast<const floatx4*>(qcol + lr * LDA + k);
+            const floatx4 b1 = *reinterpret_cast<const floatx4*>(qcol + lr * LDA + k + 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 v = *reinterpret_cast<const float4*>(P + (r0 + i) * ldp + q0);
-            pr[i][0] = v.x;
-            pr[i][1] = v.y;
-            pr[i][2] = v.z;
-            pr[i][3] = v.w;
+            for (int s = 0; s < 4; ++s) {
+                b[s] = b0[s];
+                b[s + 4] = b1[s];
+            }
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 qv = *reinterpret_cast<const float4*>(Q + (q0 + q) * ldq + c0);
-            const float qq[4] = {qv.x, qv.y, qv.z, qv.w};
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b[s], acc, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(pr[i][q], qq[j], acc[i][j]);
-        }
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b[s + 4], acc, 0, 0, 0);
     }
 }
+
+__device__ __forceinline__ int mfma_row(int e, int lane) { return 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3); }
 
 __global__ __launch_bounds__(DT) void chol_diag_kernel(float* __restrict__ W, int ld, int j0, int nb,
                                                        float* __restrict__ Xout, uint32_t* __restrict__ info) {
     __shared__ DiagLds D;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     // the lower triangle, padded with the identity.  Thread t takes column
-    // c = t % 128 of rows t / 128 + 2 i; every load is issued unconditionally
-    // from a clamped address (then masked), 16 in flight per batch.
+    // c = t % 128 of rows t / 128 + 8 i; every load is issued unconditionally
+    // from a clamped address (then masked), all 16 in flight together.
     const int cc = t & (NB - 1), rb = t >> 7;
-    const float* src = W + (size_t)j0 * ld + j0 + (cc < nb ? cc : nb - 1);
+    constexpr int RSTEP = DT / NB, RPT = NB / RSTEP;   // 8 rows apart, 16 per thread
+    {
+        const float* src = W + (size_t)j0 * ld + j0 + (cc < nb ? cc : nb - 1);
+        float v[RPT];
 #pragma unroll
-    for (int i0 = 0; i0 < NB / 2; i0 += 16) {
-        float v[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = rb + 2 * (i0 + i);
+        for (int i = 0; i < RPT; ++i) {
+            const int r = rb + RSTEP * i;
             v[i] = src[(size_t)(r < nb ? r : nb - 1) * ld];
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = rb + 2 * (i0 + i);
+        for (int i = 0; i < RPT; ++i) {
+            const int r = rb + RSTEP * i;
             const bool in = r < nb && cc < nb && cc <= r;
             D.A[r][cc] = in ? v[i] : (r == cc ? 1.0f : 0.0f);
             D.X[r][cc] = 0.0f;
@@ -181,114 +196,56 @@ __global__ __launch_bounds__(DT) void chol_diag_kernel(float* __restrict__ W, in
         __syncthreads();
         const int mi = NB - s0 - SB;   // rows below the sub-block, within the block
         if (mi <= 0) break;
-        // 2. L[i][s0 ..] = A[i][s0 ..] Y^T for the rows below: thread -> (row,
-        // 8 columns), at most two passes; results held over the barrier
-        float out[2][8];
-        int orow[2], ocol[2];
+        // 2. L = A Y^T for the rows below, in place: wave w < mi / 32 takes
+        // rows s0 + 32 (w + 1) .. + 31 (its reads of them all precede its
+        // writes; no other wave touches them)
+        const int nrt = mi / SB;
+        if (wv < nrt) {
+            const int r0 = s0 + SB * (wv + 1);
+            floatx16 acc = {};
+            mfma_block<false>(acc, &D.A[r0][s0], &D.X[s0][s0], LDA, SB / 16, lane);
 #pragma unroll
-        for (int pass = 0; pass < 2; ++pass) {
-            const int idx = t + pass * DT;
-            const int i = s0 + SB + (idx >> 2), cg = (idx & 3) * 8;
-            orow[pass] = idx < mi * 4 ? i : -1;
-            ocol[pass] = cg;
-            const int ii = idx < mi * 4 ? i : s0 + SB;
-            float ar[SB];
-#pragma unroll
-            for (int k0 = 0; k0 < SB; k0 += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(&D.A[ii][s0 + k0]);
-                ar[k0] = v.x;
-                ar[k0 + 1] = v.y;
-                ar[k0 + 2] = v.z;
-                ar[k0 + 3] = v.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float* yr = &D.X[s0 + cg + j][s0];
-                float acc = 0.0f;
-#pragma unroll
-                for (int k0 = 0; k0 < SB; k0 += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(yr + k0);
-                    acc = fmaf(ar[k0], v.x, acc);
-                    acc = fmaf(ar[k0 + 1], v.y, acc);
-                    acc = fmaf(ar[k0 + 2], v.z, acc);
-                    acc = fmaf(ar[k0 + 3], v.w, acc);
-                }
-                out[pass][j] = acc;
-            }
+            for (int e = 0; e < 16; ++e) D.A[r0 + mfma_row(e, lane)][s0 + (lane & 31)] = acc[e];
         }
         __syncthreads();
-#pragma unroll
-        for (int pass = 0; pass < 2; ++pass)
-            if (orow[pass] >= 0) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) D.A[orow[pass]][s0 + ocol[pass] + j] = out[pass][j];
-            }
-        __syncthreads();
         // 3. the trailing lower triangle: A[i][c] -= sum_k L[i][k] L[c][k],
-        // 4 x 4 tiles (tr >= tc) of the mi x mi block
-        const int tn = mi / 4, ntiles = tn * (tn + 1) / 2;
-        for (int idx = t; idx < ntiles; idx += DT) {
-            int tr = (int)((sqrtf(8.0f * (float)idx + 1.0f) - 1.0f) * 0.5f);
-            while ((tr + 1) * (tr + 2) / 2 <= idx) ++tr;
-            while (tr * (tr + 1) / 2 > idx) --tr;
-            const int tc = idx - tr * (tr + 1) / 2;
-            const int i0 = s0 + SB + 4 * tr, c0 = s0 + SB + 4 * tc;
-            float acc[4][4] = {};
+        // a wave per 32 x 32 tile (ti >= tj) of the mi x mi block
+        if (wv < nrt * (nrt + 1) / 2) {
+            int ti = 0, rem = wv;
+            while (rem > ti) rem -= ++ti;
+            const int tj = rem;
+            const int r0 = s0 + SB * (ti + 1), c0 = s0 + SB * (tj + 1);
+            floatx16 acc = {};
+            mfma_block<false>(acc, &D.A[r0][s0], &D.A[c0][s0], LDA, SB / 16, lane);
+            const int col = c0 + (lane & 31);
 #pragma unroll
-            for (int k0 = 0; k0 < SB; k0 += 4) {
-                float li[4][4], lc[4][4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 u = *reinterpret_cast<const float4*>(&D.A[i0 + q][s0 + k0]);
-                    const float4 v = *reinterpret_cast<const float4*>(&D.A[c0 + q][s0 + k0]);
-                    li[q][0] = u.x; li[q][1] = u.y; li[q][2] = u.z; li[q][3] = u.w;
-                    lc[q][0] = v.x; lc[q][1] = v.y; lc[q][2] = v.z; lc[q][3] = v.w;
-                }
-#pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(li[i][kk], lc[j][kk], acc[i][j]);
+            for (int e = 0; e < 16; ++e) {
+                const int row = r0 + mfma_row(e, lane);
+                if (col <= row) D.A[row][col] -= acc[e];
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (c0 + j <= i0 + i) D.A[i0 + i][c0 + j] -= acc[i][j];
         }
         __syncthreads();
     }
 
-    // X's off-diagonal blocks: round dd computes X_ip for i - p = dd
+    // X's off-diagonal blocks: round dd computes X_ip for i - p = dd, a wave
+    // per block: S = sum_{k=p}^{i-1} L_ik X_kp (one 32 dd long sum), then
+    // X_ip = -Y_i S
 #pragma unroll
     for (int dd = 1; dd < NB / SB; ++dd) {
         const int nblk = NB / SB - dd;   // blocks this round (<= 3)
-        // S_b = sum_{k=p}^{i-1} L_ik X_kp; thread -> one 4 x 4 tile of one block
-        if (t < nblk * 64) {
-            const int bidx = t >> 6, tile = t & 63;
-            const int p = bidx, i = p + dd;
-            const int r0 = (tile >> 3) * 4, c0 = (tile & 7) * 4;
-            float acc[4][4] = {};
-            for (int k = p; k < i; ++k)
-                tile_mm(acc, &D.A[i * SB][k * SB], LDA, &D.X[k * SB][p * SB], LDA, r0, c0);
+        const int p = wv, i = p + dd;
+        if (wv < nblk) {
+            floatx16 acc = {};
+            mfma_block<true>(acc, &D.A[i * SB][p * SB], &D.X[p * SB][p * SB], LDA, 2 * dd, lane);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) D.S[bidx][r0 + q][c0 + j] = acc[q][j];
+            for (int e = 0; e < 16; ++e) D.S[wv][mfma_row(e, lane)][lane & 31] = acc[e];
         }
         __syncthreads();
-        // X_ip = -Y_i S_b
-        if (t < nblk * 64) {
-            const int bidx = t >> 6, tile = t & 63;
-            const int p = bidx, i = p + dd;
-            const int r0 = (tile >> 3) * 4, c0 = (tile & 7) * 4;
-            float acc[4][4] = {};
-            tile_mm(acc, &D.X[i * SB][i * SB], LDA, &D.S[bidx][0][0], SB + 4, r0, c0);
+        if (wv < nblk) {
+            floatx16 acc = {};
+            mfma_block<true>(acc, &D.X[i * SB][i * SB], &D.S[wv][0][0], SB + 4, SB / 16, lane);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) D.X[i * SB + r0 + q][p * SB + c0 + j] = -acc[q][j];
+            for (int e = 0; e < 16; ++e) D.X[i * SB + mfma_row(e, lane)][p * SB + (lane & 31)] = -acc[e];
         }
         __syncthreads();
     }
@@ -296,9 +253,9 @@ __global__ __launch_bounds__(DT) void chol_diag_kernel(float* __restrict__ W, in
     // L (lower, diagonal included) back to W; X out (nb x nb)
     if (cc < nb) {
         float* dst = W + (size_t)j0 * ld + j0 + cc;
-#pragma unroll 8
-        for (int i = 0; i < NB / 2; ++i) {
-            const int r = rb + 2 * i;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int r = rb + RSTEP * i;
             if (r < nb) {
                 if (cc <= r) dst[(size_t)r * ld] = D.A[r][cc];
                 Xout[(size_t)r * nb + cc] = D.X[r][cc];
@@ -356,7 +313,7 @@ void chol_blocked(const float* a, float* l, uint32_t* info, float* work, float* 
             const int nb = nn - j < NB ? nn - j : NB;
             {
                 KernelTimer t("chol_diag", s);
-                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(256), 0, s, W, nn, j, nb, xinv, inf);
+                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(DT), 0, s, W, nn, j, nb, xinv, inf);
                 t.stop();
             }
             const int m2 = nn - j - nb;

@@ -33,6 +33,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int LP = BK + 4;   // LDS pitch (floats): conflict-free b128 reads
+// below this many 128 x 128 tiles a K <= 128 product takes the 64 x 64 kernel
+constexpr uint64_t kSmallTiles = 512;
 
 struct GemmArgs {
     const float* A;
@@ -230,6 +232,133 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         }
 }
 
+// Small-K products (K <= 128: the rank-nb trailing updates and TRSMs of the
+// blocked factorisations), where the 128 x 128 kernel's K loop is a chain of
+// global-load latencies and its tiles too few to fill the chip.  A
+// 256-thread workgroup computes a 64 x 64 tile of C, each wave one 32 x 32
+// MFMA block; the whole K extent of both operands is loaded at once (every
+// load in flight together) into LDS, [row][k] with pitch KP, then fed to the
+// matrix cores with the same permuted-k reads as above.
+constexpr int SM = 64, SK = 128, KP = SK + 4;
+
+template <bool TRANS, bool VEC>
+__device__ __forceinline__ void load_panel(const float* __restrict__ p, int ld, int rows, int K, int r0,
+                                           float (*s)[KP]) {
+    const int t = threadIdx.x;
+    float v[8][4];
+    if (!TRANS) {
+        // 32 float4 per row (k = 4q): thread t takes (row, q) = (idx / 32, idx % 32)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + 256 * i, r = r0 + (idx >> 5), k = (idx & 31) * 4;
+            if (VEC) {
+                const bool in = r < rows && k < K;
+                const floatx4 x = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)r * ld + k : 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = in ? x[e] : 0.0f;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool in = r < rows && k + e < K;
+                    const float x = p[in ? (size_t)r * ld + k + e : 0];
+                    v[i][e] = in ? x : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + 256 * i;
+            floatx4 x = {v[i][0], v[i][1], v[i][2], v[i][3]};
+            *reinterpret_cast<floatx4*>(&s[idx >> 5][(idx & 31) * 4]) = x;
+        }
+    } else {
+        // stored [k][row]: thread t takes rows 4q .. 4q+3 of one k, (k, q) =
+        // (idx / 16, idx % 16): a wave reads 4 k of 64 consecutive rows
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + 256 * i, k = idx >> 4, r = r0 + (idx & 15) * 4;
+            if (VEC) {
+                const bool in = k < K && r < rows;
+                const floatx4 x = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)k * ld + r : 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = in ? x[e] : 0.0f;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool in = k < K && r + e < rows;
+                    const float x = p[in ? (size_t)k * ld + r + e : 0];
+                    v[i][e] = in ? x : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = t + 256 * i, k = idx >> 4, rq = (idx & 15) * 4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[rq + e][k] = v[i][e];
+        }
+    }
+}
+
+template <bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(256) void gemm_k128_kernel(GemmArgs g) {
+    __shared__ float As[SM][KP];
+    __shared__ float Bs[SM][KP];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+    const int m0 = blockIdx.y * SM, n0 = blockIdx.x * SM;
+    if (g.lower && n0 >= m0 + SM) return;   // tile strictly above the diagonal (uniform)
+    const size_t bz = blockIdx.z;
+    const float* A = g.A + bz * g.sa;
+    const float* B = g.B + bz * g.sb;
+    float* C = g.C + bz * g.sc;
+
+    load_panel<TA, VEC>(A, g.lda, g.M, g.K, m0, As);
+    load_panel<!TB, VEC>(B, g.ldb, g.N, g.K, n0, Bs);
+    __syncthreads();
+
+    floatx16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    const int lr = lane & 31;
+    const int kh = (lane >> 5) * 8;
+    const int ktiles = (g.K + 15) / 16;
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int kb = kt * 16 + kh;
+        const floatx4 a0 = *reinterpret_cast<const floatx4*>(&As[wm + lr][kb]);
+        const floatx4 a1 = *reinterpret_cast<const floatx4*>(&As[wm + lr][kb + 4]);
+        const floatx4 b0 = *reinterpret_cast<const floatx4*>(&Bs[wn + lr][kb]);
+        const floatx4 b1 = *reinterpret_cast<const floatx4*>(&Bs[wn + lr][kb + 4]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc, 0, 0, 0);
+    }
+
+    const bool keep = g.beta != 0.0f;
+    const int col = n0 + wn + lr;
+    const bool cin = col < g.N;
+    float cv[16];
+    if (keep) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = m0 + wm + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const bool in = cin && row < g.M;
+            cv[e] = C[in ? (size_t)row * g.ldc + col : 0];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (cin && row < g.M) {
+            const float v = g.alpha * acc[e];
+            C[(size_t)row * g.ldc + col] = keep ? fmaf(g.beta, cv[e], v) : v;
+        }
+    }
+}
+
 }  // namespace
 
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
@@ -239,6 +368,10 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
     GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta, lower_only ? 1 : 0};
     const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
     KernelTimer t("gemm_mfma", s);
+    // K <= 128 with fewer than kSmallTiles 128 x 128 tiles: the 64 x 64
+    // whole-K kernel (four times the workgroups, one load latency)
+    const bool small = K <= SK && (uint64_t)grid.x * grid.y * grid.z < kSmallTiles;
+    const dim3 sgrid((unsigned)cdiv(N, SM), (unsigned)cdiv(M, SM), (unsigned)batch);
     // float4 operand loads: 16-byte aligned bases, strides and leading
     // dimensions, and the contiguous extent of each operand a multiple of 4
     auto al = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
@@ -246,7 +379,9 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
                      ((ta ? M : K) & 3) == 0 && ((tb ? K : N) & 3) == 0;
 #define MLA_GEMM_LAUNCH(TA_, TB_)                                                                       \
     do {                                                                                                \
-        if (vec) hipLaunchKernelGGL((gemm_kernel<TA_, TB_, true>), grid, dim3(256), 0, s, g);           \
+        if (small && vec) hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, true>), sgrid, dim3(256), 0, s, g); \
+        else if (small) hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, false>), sgrid, dim3(256), 0, s, g); \
+        else if (vec) hipLaunchKernelGGL((gemm_kernel<TA_, TB_, true>), grid, dim3(256), 0, s, g);      \
         else hipLaunchKernelGGL((gemm_kernel<TA_, TB_, false>), grid, dim3(256), 0, s, g);              \
     } while (0)
     if (!ta && !tb) MLA_GEMM_LAUNCH(false, false);

@@ -1,6 +1,9 @@
 """The fp32 MFMA GEMM the blocked factorisations build on, against a float64
 product: every transpose combination, ragged edges, strided batches,
-alpha/beta.  Bound per element: 2 K eps (|A||B|)_ij + eps |beta C_ij|."""
+alpha/beta.  Bound per element: 2 K eps (|A||B|)_ij + eps |beta C_ij|.
+Products with K <= 128 on a small grid run the 64 x 64 whole-K kernel
+(every case here with K <= 128 except 2900 x 2900 x 64, which has enough
+128 x 128 tiles to stay on the main kernel)."""
 
 import ctypes
 
@@ -26,7 +29,7 @@ def run(lib, ta, tb, a, b, c, alpha, beta, batch=1):
 @pytest.mark.parametrize("ta", [False, True])
 @pytest.mark.parametrize("tb", [False, True])
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (128, 128, 16), (130, 70, 33), (257, 384, 100), (64, 513, 7),
-                                   (600, 200, 257)])
+                                   (600, 200, 257), (200, 300, 128), (2900, 2900, 64)])
 def test_gemm(cuda, lib, ta, tb, m, n, k):
     rng = np.random.default_rng(m * 7 + n * 3 + k)
     batch = 2
