@@ -235,21 +235,26 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 // Small-K products (K <= 128: the rank-nb trailing updates and TRSMs of the
 // blocked factorisations), where the 128 x 128 kernel's K loop is a chain of
 // global-load latencies and its tiles too few to fill the chip.  A
-// 256-thread workgroup computes a 64 x 64 tile of C, each wave one 32 x 32
-// MFMA block; the whole K extent of both operands is loaded at once (every
-// load in flight together) into LDS, [row][k] with pitch KP, then fed to the
-// matrix cores with the same permuted-k reads as above.
+// 256-thread workgroup computes a TM x TN tile of C (64 x 64, or 32 x 128
+// for an in-place product with N <= 128), a wave per 32 x 32 MFMA block; the whole
+// K extent of both operands is loaded at once (every load in flight
+// together) into LDS, [row][k] with pitch KP, then fed to the matrix cores
+// with the same permuted-k reads as above.  With a tile as wide as N, a
+// workgroup has read its rows of A whole before it writes C, so C may be A
+// itself (an in-place product).
 constexpr int SM = 64, SK = 128, KP = SK + 4;
 
-template <bool TRANS, bool VEC>
+template <bool TRANS, bool VEC, int ROWS>
 __device__ __forceinline__ void load_panel(const float* __restrict__ p, int ld, int rows, int K, int r0,
                                            float (*s)[KP]) {
+    constexpr int IT = ROWS / 8;   // float4 per thread: ROWS x 128 floats over 256 threads
+    static_assert(IT >= 1 && ROWS % 32 == 0, "panel rows");
     const int t = threadIdx.x;
-    float v[8][4];
+    float v[IT][4];
     if (!TRANS) {
         // 32 float4 per row (k = 4q): thread t takes (row, q) = (idx / 32, idx % 32)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < IT; ++i) {
             const int idx = t + 256 * i, r = r0 + (idx >> 5), k = (idx & 31) * 4;
             if (VEC) {
                 const bool in = r < rows && k < K;
@@ -266,17 +271,19 @@ __device__ __forceinline__ void load_panel(const float* __restrict__ p, int ld, 
             }
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < IT; ++i) {
             const int idx = t + 256 * i;
             floatx4 x = {v[i][0], v[i][1], v[i][2], v[i][3]};
             *reinterpret_cast<floatx4*>(&s[idx >> 5][(idx & 31) * 4]) = x;
         }
     } else {
         // stored [k][row]: thread t takes rows 4q .. 4q+3 of one k, (k, q) =
-        // (idx / 16, idx % 16): a wave reads 4 k of 64 consecutive rows
+        // (idx / (ROWS / 4), idx % (ROWS / 4)): consecutive threads read
+        // consecutive rows of one k
+        constexpr int QR = ROWS / 4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = t + 256 * i, k = idx >> 4, r = r0 + (idx & 15) * 4;
+        for (int i = 0; i < IT; ++i) {
+            const int idx = t + 256 * i, k = idx / QR, r = r0 + (idx % QR) * 4;
             if (VEC) {
                 const bool in = k < K && r < rows;
                 const floatx4 x = *reinterpret_cast<const floatx4*>(p + (in ? (size_t)k * ld + r : 0));
@@ -292,36 +299,41 @@ __device__ __forceinline__ void load_panel(const float* __restrict__ p, int ld, 
             }
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = t + 256 * i, k = idx >> 4, rq = (idx & 15) * 4;
+        for (int i = 0; i < IT; ++i) {
+            const int idx = t + 256 * i, k = idx / QR, rq = (idx % QR) * 4;
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[rq + e][k] = v[i][e];
         }
     }
 }
 
-template <bool TA, bool TB, bool VEC>
+template <bool TA, bool TB, bool VEC, int TM, int TN>
 __global__ __launch_bounds__(256) void gemm_k128_kernel(GemmArgs g) {
-    __shared__ float As[SM][KP];
-    __shared__ float Bs[SM][KP];
+    constexpr int WM = TM / 32, WN = 4 / WM;   // the four waves as WM x WN
+    constexpr int NBW = TN / WN / 32;          // 32 x 32 blocks per wave along N
+    static_assert(NBW >= 1 && WM * WN == 4, "tile shape");
+    __shared__ float As[TM][KP];
+    __shared__ float Bs[TN][KP];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
-    const int m0 = blockIdx.y * SM, n0 = blockIdx.x * SM;
-    if (g.lower && n0 >= m0 + SM) return;   // tile strictly above the diagonal (uniform)
+    const int wm = (wave % WM) * 32, wn = (wave / WM) * (TN / WN);
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+    if (g.lower && n0 >= m0 + TM) return;   // tile strictly above the diagonal (uniform)
     const size_t bz = blockIdx.z;
     const float* A = g.A + bz * g.sa;
     const float* B = g.B + bz * g.sb;
     float* C = g.C + bz * g.sc;
 
-    load_panel<TA, VEC>(A, g.lda, g.M, g.K, m0, As);
-    load_panel<!TB, VEC>(B, g.ldb, g.N, g.K, n0, Bs);
+    load_panel<TA, VEC, TM>(A, g.lda, g.M, g.K, m0, As);
+    load_panel<!TB, VEC, TN>(B, g.ldb, g.N, g.K, n0, Bs);
     __syncthreads();
 
-    floatx16 acc;
+    floatx16 acc[NBW];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+    for (int j = 0; j < NBW; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
     const int lr = lane & 31;
     const int kh = (lane >> 5) * 8;
     const int ktiles = (g.K + 15) / 16;
@@ -329,34 +341,68 @@ __global__ __launch_bounds__(256) void gemm_k128_kernel(GemmArgs g) {
         const int kb = kt * 16 + kh;
         const floatx4 a0 = *reinterpret_cast<const floatx4*>(&As[wm + lr][kb]);
         const floatx4 a1 = *reinterpret_cast<const floatx4*>(&As[wm + lr][kb + 4]);
-        const floatx4 b0 = *reinterpret_cast<const floatx4*>(&Bs[wn + lr][kb]);
-        const floatx4 b1 = *reinterpret_cast<const floatx4*>(&Bs[wn + lr][kb + 4]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc, 0, 0, 0);
+        for (int j = 0; j < NBW; ++j) {
+            const floatx4 b0 = *reinterpret_cast<const floatx4*>(&Bs[wn + 32 * j + lr][kb]);
+            const floatx4 b1 = *reinterpret_cast<const floatx4*>(&Bs[wn + 32 * j + lr][kb + 4]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc, 0, 0, 0);
+            for (int s = 0; s < 4; ++s) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[s], b0[s], acc[j], 0, 0, 0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[s], b1[s], acc[j], 0, 0, 0);
+        }
     }
 
     const bool keep = g.beta != 0.0f;
-    const int col = n0 + wn + lr;
-    const bool cin = col < g.N;
-    float cv[16];
-    if (keep) {
+#pragma unroll
+    for (int j = 0; j < NBW; ++j) {
+        const int col = n0 + wn + 32 * j + lr;
+        const bool cin = col < g.N;
+        float cv[16];
+        if (keep) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const bool in = cin && row < g.M;
+                cv[e] = C[in ? (size_t)row * g.ldc + col : 0];
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int row = m0 + wm + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            const bool in = cin && row < g.M;
-            cv[e] = C[in ? (size_t)row * g.ldc + col : 0];
+            if (cin && row < g.M) {
+                const float v = g.alpha * acc[j][e];
+                C[(size_t)row * g.ldc + col] = keep ? fmaf(g.beta, cv[e], v) : v;
+            }
         }
     }
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (cin && row < g.M) {
-            const float v = g.alpha * acc[e];
-            C[(size_t)row * g.ldc + col] = keep ? fmaf(g.beta, cv[e], v) : v;
+}
+
+// Whether two strided row-major blocks (rows x cols, leading dimension ld,
+// `nb` of them `stride` floats apart) share an element.  With one block each
+// and equal leading dimensions the test is exact (two rectangles of the same
+// row grid, the second's columns possibly wrapping into the next row), so
+// that neighbouring blocks of one matrix (a panel and its trailing block)
+// are told apart; otherwise the address ranges are compared.
+bool blocks_overlap(const float* p, long long rows, long long cols, int ld, long long stride, const float* q,
+                    long long qrows, long long qcols, int qld, long long qstride, int nb) {
+    if (rows <= 0 || cols <= 0 || qrows <= 0 || qcols <= 0) return false;
+    if (nb == 1 && ld == qld && cols <= ld && qcols <= ld) {
+        const long long d = (long long)(q - p);   // q's first element on p's grid
+        long long dr = d / ld, dc = d % ld;
+        if (dc < 0) {
+            dc += ld;
+            --dr;
         }
+        auto hit = [&](long long r0, long long r1, long long c0, long long c1) {   // [r0, r1) x [c0, c1)
+            return r0 < rows && 0 < r1 && c0 < cols && 0 < c1;
+        };
+        if (dc + qcols <= ld) return hit(dr, dr + qrows, dc, dc + qcols);
+        return hit(dr, dr + qrows, dc, ld) || hit(dr + 1, dr + qrows + 1, 0, dc + qcols - ld);
     }
+    const uintptr_t p0 = (uintptr_t)p, q0 = (uintptr_t)q;
+    const uintptr_t p1 = (uintptr_t)(p + (nb - 1) * stride + (rows - 1) * ld + cols);
+    const uintptr_t q1 = (uintptr_t)(q + (nb - 1) * qstride + (qrows - 1) * qld + qcols);
+    return p0 < q1 && q0 < p1;
 }
 
 }  // namespace
@@ -369,9 +415,25 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
     const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
     KernelTimer t("gemm_mfma", s);
     // K <= 128 with fewer than kSmallTiles 128 x 128 tiles: the 64 x 64
-    // whole-K kernel (four times the workgroups, one load latency)
-    const bool small = K <= SK && (uint64_t)grid.x * grid.y * grid.z < kSmallTiles;
-    const dim3 sgrid((unsigned)cdiv(N, SM), (unsigned)cdiv(M, SM), (unsigned)batch);
+    // whole-K kernel (four times the workgroups, one load latency) -- unless
+    // C overlaps an operand (an in-place product such as the blocked
+    // Cholesky's L21 = A21 X^T): its 64-column tiles would let one
+    // workgroup overwrite rows of A that another still reads, whereas a
+    // single 128-column tile reads its rows whole before writing them
+    auto over_a_or_b = [&](const float* p, long long rows, long long cols, int ld, long long stride) {
+        return blocks_overlap(p, rows, cols, ld, stride, C, M, N, ldc, sc, batch);
+    };
+    const bool over_a = over_a_or_b(A, ta ? K : M, ta ? M : K, lda, sa);
+    const bool over_b = over_a_or_b(B, tb ? N : K, tb ? K : N, ldb, sb);
+    // C = A itself, row for row, with N <= 128: tiles as wide as N (32 x
+    // 128, or 64 x 64 for N <= 64) read each row of A whole before writing
+    // it, and no other workgroup touches it
+    const bool same_rows = over_a && !over_b && C == A && !ta && ldc == lda && sc == sa && N <= 128;
+    const bool small = K <= SK && (!(over_a || over_b) || same_rows) &&
+                       (uint64_t)grid.x * grid.y * grid.z < kSmallTiles;
+    const bool wide = same_rows && N > SM;   // the 32 x 128 tiles
+    const int tm = wide ? 32 : SM, tn = wide ? 128 : SM;
+    const dim3 sgrid((unsigned)cdiv(N, tn), (unsigned)cdiv(M, tm), (unsigned)batch);
     // float4 operand loads: 16-byte aligned bases, strides and leading
     // dimensions, and the contiguous extent of each operand a multiple of 4
     auto al = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
@@ -379,8 +441,14 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
                      ((ta ? M : K) & 3) == 0 && ((tb ? K : N) & 3) == 0;
 #define MLA_GEMM_LAUNCH(TA_, TB_)                                                                       \
     do {                                                                                                \
-        if (small && vec) hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, true>), sgrid, dim3(256), 0, s, g); \
-        else if (small) hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, false>), sgrid, dim3(256), 0, s, g); \
+        if (small && wide && vec)                                                                       \
+            hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, true, 32, 128>), sgrid, dim3(256), 0, s, g); \
+        else if (small && wide)                                                                         \
+            hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, false, 32, 128>), sgrid, dim3(256), 0, s, g);\
+        else if (small && vec)                                                                          \
+            hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, true, 64, 64>), sgrid, dim3(256), 0, s, g);  \
+        else if (small)                                                                                 \
+            hipLaunchKernelGGL((gemm_k128_kernel<TA_, TB_, false, 64, 64>), sgrid, dim3(256), 0, s, g); \
         else if (vec) hipLaunchKernelGGL((gemm_kernel<TA_, TB_, true>), grid, dim3(256), 0, s, g);      \
         else hipLaunchKernelGGL((gemm_kernel<TA_, TB_, false>), grid, dim3(256), 0, s, g);              \
     } while (0)

@@ -54,3 +54,24 @@ def test_gemm_beta_zero_ignores_c(cuda, lib):
     c = np.full((70, 90), np.nan, np.float32)
     run(lib, False, False, a, b, c, np.float32(1), np.float32(0))
     assert np.abs(c - a.astype(np.float64) @ b).max() <= 1e-4
+
+
+@pytest.mark.parametrize("m", [100, 2000])
+def test_gemm_in_place(cuda, lib, m):
+    """C = A X^T written over A (device memory, as the blocked Cholesky's
+    L21 = A21 X^T): every row of A is read whole before it is overwritten."""
+    torch = cuda
+    rng = np.random.default_rng(m)
+    a = rng.standard_normal((m, 128)).astype(np.float32)
+    x = rng.standard_normal((128, 128)).astype(np.float32)
+    ref = a.astype(np.float64) @ x.astype(np.float64).T
+    ad = torch.from_numpy(a).to("cuda")
+    xd = torch.from_numpy(x).to("cuda")
+    rc = lib.hip_sgemm(0, 1, m, 128, 128, np.float32(1), ad.data_ptr(), 128, 0, xd.data_ptr(), 128, 0,
+                       np.float32(0), ad.data_ptr(), 128, 0, 1)
+    assert rc == 0, lib.last_error()
+    torch.cuda.synchronize()
+    out = ad.cpu().numpy()
+    mag = np.abs(a).astype(np.float64) @ np.abs(x).T
+    eps = np.finfo(np.float32).eps
+    assert np.all(np.abs(out - ref) <= 2 * 130 * eps * mag)
