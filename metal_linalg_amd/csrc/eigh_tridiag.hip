@@ -317,11 +317,19 @@ __global__ __launch_bounds__(256) void fill_nan_kernel(float* __restrict__ x, si
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) x[i] = qnan();
 }
 
+// out[i] = sum over b of part[b count + i], in order of b; eight partials in
+// flight at a time (indices past the last read it again and add zero)
 __global__ __launch_bounds__(256) void sum_parts2_kernel(const float* __restrict__ part, int nsplit, size_t count,
                                                          float* __restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
         float s = 0.0f;
-        for (int b = 0; b < nsplit; ++b) s += part[(size_t)b * count + i];
+        for (int b0 = 0; b0 < nsplit; b0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = part[(size_t)min(b0 + j, nsplit - 1) * count + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += v[j] * (b0 + j < nsplit ? 1.0f : 0.0f);
+        }
         out[i] = s;
     }
 }
@@ -332,23 +340,20 @@ __global__ void set_info_kernel(uint32_t* info, const uint32_t* flags) {
 
 unsigned grid_of(size_t count) { return (unsigned)std::min<size_t>(cdiv(count, 256), 4096); }
 
-constexpr int kRowChunk = 512;
+constexpr int kRowChunk = 128;   // rows of a split-K chunk: the small-K GEMM's whole K
 
 // C (M x N) = A B over a long K, split in chunks summed afterwards (the
 // products with V^T over many rows): A M x K (row-major, lda); B K x N
 // (ldb), or with tb stored N x K
 void split_rows_gemm(bool tb, int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* part,
                      float* C, hipStream_t s) {
-    const int full = K / kRowChunk, rest = K - full * kRowChunk;
+    // one batched launch over chunks of kRowChunk rows of the sum (the last
+    // one shorter), then the partials added in order
+    const int nsplit = (K + kRowChunk - 1) / kRowChunk;
+    const int last = K - (nsplit - 1) * kRowChunk;
     const long long sb = tb ? kRowChunk : (long long)kRowChunk * ldb;
-    if (full > 0)
-        sgemm(false, tb, M, N, kRowChunk, 1.0f, A, lda, kRowChunk, B, ldb, sb, 0.0f, part, N, (long long)M * N, full,
-              s);
-    if (rest > 0)
-        sgemm(false, tb, M, N, rest, 1.0f, A + (size_t)full * kRowChunk, lda, 0,
-              B + (tb ? (size_t)full * kRowChunk : (size_t)full * kRowChunk * ldb), ldb, 0, 0.0f,
-              part + (size_t)full * M * N, N, 0, 1, s);
-    const int nsplit = full + (rest > 0 ? 1 : 0);
+    sgemm(false, tb, M, N, kRowChunk, 1.0f, A, lda, kRowChunk, B, ldb, sb, 0.0f, part, N, (long long)M * N, nsplit, s,
+          false, last);
     hipLaunchKernelGGL(sum_parts2_kernel, dim3(grid_of((size_t)M * N)), dim3(256), 0, s, part, nsplit, (size_t)M * N,
                        C);
 }

@@ -33,7 +33,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int LP = BK + 4;   // LDS pitch (floats): conflict-free b128 reads
-// below this many 128 x 128 tiles a K <= 128 product takes the 64 x 64 kernel
+// below this many 128 x 128 tiles per batch entry a K <= 128 product takes
+// the 64 x 64 kernel
 constexpr uint64_t kSmallTiles = 512;
 
 struct GemmArgs {
@@ -45,6 +46,7 @@ struct GemmArgs {
     long long sa, sb, sc;   // batch strides (floats)
     float alpha, beta;
     int lower;   // 1: only tiles that reach the lower triangle (row >= col) of C
+    int K_last;  // K of the last batch entry (a split-K batch's shorter tail)
 };
 
 // Loads this thread's share of a 128 x 16 operand tile (rows r0.., k0..) into
@@ -155,6 +157,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const float* A = g.A + bz * g.sa;
     const float* B = g.B + bz * g.sb;
     float* C = g.C + bz * g.sc;
+    const int K = blockIdx.z + 1 == gridDim.z ? g.K_last : g.K;
 
     floatx16 acc[2][2];
 #pragma unroll
@@ -165,20 +168,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     float ra[8], rb[8];
-    load_tile<TA, VEC>(A, g.lda, g.M, g.K, m0, 0, ra);
-    load_tile<!TB, VEC>(B, g.ldb, g.N, g.K, n0, 0, rb);
+    load_tile<TA, VEC>(A, g.lda, g.M, K, m0, 0, ra);
+    load_tile<!TB, VEC>(B, g.ldb, g.N, K, n0, 0, rb);
     store_tile<TA>(As[0], ra);
     store_tile<!TB>(Bs[0], rb);
     __syncthreads();
 
-    const int ktiles = (g.K + BK - 1) / BK;
+    const int ktiles = (K + BK - 1) / BK;
     const int lr = lane & 31;         // row (A) / column (B) within a 32-block
     const int kh = (lane >> 5) * 8;   // this lane's 8 k values of the tile
     for (int kt = 0; kt < ktiles; ++kt) {
         const int cur = kt & 1;
         // the next tile (past the end: all masked, no branch)
-        load_tile<TA, VEC>(A, g.lda, g.M, g.K, m0, (kt + 1) * BK, ra);
-        load_tile<!TB, VEC>(B, g.ldb, g.N, g.K, n0, (kt + 1) * BK, rb);
+        load_tile<TA, VEC>(A, g.lda, g.M, K, m0, (kt + 1) * BK, ra);
+        load_tile<!TB, VEC>(B, g.ldb, g.N, K, n0, (kt + 1) * BK, rb);
         floatx4 a0[2][2], b0[2][2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -324,9 +327,10 @@ __global__ __launch_bounds__(256) void gemm_k128_kernel(GemmArgs g) {
     const float* A = g.A + bz * g.sa;
     const float* B = g.B + bz * g.sb;
     float* C = g.C + bz * g.sc;
+    const int K = blockIdx.z + 1 == gridDim.z ? g.K_last : g.K;
 
-    load_panel<TA, VEC, TM>(A, g.lda, g.M, g.K, m0, As);
-    load_panel<!TB, VEC, TN>(B, g.ldb, g.N, g.K, n0, Bs);
+    load_panel<TA, VEC, TM>(A, g.lda, g.M, K, m0, As);
+    load_panel<!TB, VEC, TN>(B, g.ldb, g.N, K, n0, Bs);
     __syncthreads();
 
     floatx16 acc[NBW];
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(256) void gemm_k128_kernel(GemmArgs g) {
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
     const int lr = lane & 31;
     const int kh = (lane >> 5) * 8;
-    const int ktiles = (g.K + 15) / 16;
+    const int ktiles = (K + 15) / 16;
     for (int kt = 0; kt < ktiles; ++kt) {
         const int kb = kt * 16 + kh;
         const floatx4 a0 = *reinterpret_cast<const floatx4*>(&As[wm + lr][kb]);
@@ -409,12 +413,13 @@ bool blocks_overlap(const float* p, long long rows, long long cols, int ld, long
 
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
            const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
-           hipStream_t s, bool lower_only) {
+           hipStream_t s, bool lower_only, int k_last) {
     if (M <= 0 || N <= 0 || batch <= 0) return;
-    GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta, lower_only ? 1 : 0};
+    GemmArgs g{A, B, C, M, N, K, lda, ldb, ldc, sa, sb, sc, alpha, beta, lower_only ? 1 : 0,
+               k_last >= 0 ? k_last : K};
     const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)batch);
     KernelTimer t("gemm_mfma", s);
-    // K <= 128 with fewer than kSmallTiles 128 x 128 tiles: the 64 x 64
+    // K <= 128 with fewer than kSmallTiles 128 x 128 tiles per entry: the 64 x 64
     // whole-K kernel (four times the workgroups, one load latency) -- unless
     // C overlaps an operand (an in-place product such as the blocked
     // Cholesky's L21 = A21 X^T): its 64-column tiles would let one
@@ -429,8 +434,7 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
     // 128, or 64 x 64 for N <= 64) read each row of A whole before writing
     // it, and no other workgroup touches it
     const bool same_rows = over_a && !over_b && C == A && !ta && ldc == lda && sc == sa && N <= 128;
-    const bool small = K <= SK && (!(over_a || over_b) || same_rows) &&
-                       (uint64_t)grid.x * grid.y * grid.z < kSmallTiles;
+    const bool small = K <= SK && (!(over_a || over_b) || same_rows) && (uint64_t)grid.x * grid.y < kSmallTiles;
     const bool wide = same_rows && N > SM;   // the 32 x 128 tiles
     const int tm = wide ? 32 : SM, tn = wide ? 128 : SM;
     const dim3 sgrid((unsigned)cdiv(N, tn), (unsigned)cdiv(M, tm), (unsigned)batch);
@@ -438,7 +442,8 @@ void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, i
     // dimensions, and the contiguous extent of each operand a multiple of 4
     auto al = [](const void* p) { return (((uintptr_t)p) & 15) == 0; };
     const bool vec = al(A) && al(B) && (lda & 3) == 0 && (ldb & 3) == 0 && (sa & 3) == 0 && (sb & 3) == 0 &&
-                     ((ta ? M : K) & 3) == 0 && ((tb ? K : N) & 3) == 0;
+                     ((ta ? M : K) & 3) == 0 && ((tb ? K : N) & 3) == 0 && ((ta ? M : g.K_last) & 3) == 0 &&
+                     ((tb ? g.K_last : N) & 3) == 0;
 #define MLA_GEMM_LAUNCH(TA_, TB_)                                                                       \
     do {                                                                                                \
         if (small && wide && vec)                                                                       \

@@ -141,8 +141,9 @@ void svd_mid(const float* a, float* u, float* s, float* vt, uint32_t* info, uint
              hipStream_t st);
 
 // ---- fp32 MFMA GEMM: C = alpha op(A) op(B) + beta C, row-major, strided batches ----
+// k_last >= 0: the last batch entry's K (a split-K batch whose tail is shorter)
 void sgemm(bool ta, bool tb, int M, int N, int K, float alpha, const float* A, int lda, long long sa,
            const float* B, int ldb, long long sb, float beta, float* C, int ldc, long long sc, int batch,
-           hipStream_t s, bool lower_only = false);
+           hipStream_t s, bool lower_only = false, int k_last = -1);
 
 }  // namespace mla
