@@ -66,10 +66,24 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
     // tall matrices of at most 64 columns: the batched tall kernel (a tree
     // of 128-row blocks past 128 rows)
     const bool tall = !small && qr_tall_fits(M, N, QC);
-    if (!small && !tall && !qr_blocked_fits(M, N))
-        invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) +
-                ": this build's QR kernels take at most 4096 rows beyond 64 columns");
+    // beyond the blocked QR's 4096 rows: a tree of blocked QRs, to 2048 columns
+    const bool tree = !small && !tall && !qr_blocked_fits(M, N) && qr_tsqr_fits(M, N, QC);
+    if (!small && !tall && !tree && !qr_blocked_fits(M, N))
+        invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) + (mode == QrMode::complete ? " complete" : "") +
+                ": this build's QR kernels take at most 4096 rows beyond 64 columns, or any number of rows "
+                "with at most 2048 columns (reduced or R only)");
     Call call;
+    if (tree) {
+        const size_t per = (size_t)M * N;
+        const float* da = call.in(a.data, (size_t)B * per);
+        float* dq = QC ? call.out(q, (size_t)B * per) : nullptr;
+        float* dr = call.out(r, (size_t)B * N * N);
+        float* work = static_cast<float*>(call.scratch(qr_tsqr_workspace(M, N, QC != 0)));
+        for (uint32_t b = 0; b < B; ++b)
+            qr_tsqr_one(da + b * per, dq ? dq + b * per : nullptr, dr + (size_t)b * N * N, M, N, work, call.stream());
+        call.finish();
+        return;
+    }
     if (small || tall) {
         const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)M * N * 4},
                                              {nullptr, QC ? q : nullptr, (size_t)M * QC * 4},
@@ -286,7 +300,8 @@ void svd(const Matrices& a, float* u, float* s, float* vt, uint32_t* info) {
         }
         if (!svd_large_fits(M, N))
             invalid("[svd] " + std::to_string(M) + "x" + std::to_string(N) +
-                    ": this build's SVD kernels take max(M, N) <= 4096");
+                    ": this build's SVD kernels take min(M, N) <= 64 at any length, max(M, N) <= 4096, or "
+                    "min(M, N) <= 2048 beyond");
         Call call;
         const size_t per = (size_t)M * N;
         const float* da = call.in(a.data, (size_t)B * per);

@@ -31,6 +31,12 @@ size_t qr_blocked_workspace(uint32_t m, uint32_t n);
 void qr_blocked(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, uint32_t qc, uint32_t rr,
                 float* work, hipStream_t s);
 
+// ---- QR of one matrix beyond the blocked QR's rows (m > 4096, n <= 2048), a tree of blocked QRs ----
+// q (m x n) or NULL for R alone; r n x n; work = qr_tsqr_workspace(m, n, q != NULL) bytes.
+bool qr_tsqr_fits(uint32_t m, uint32_t n, uint32_t qc);
+size_t qr_tsqr_workspace(uint32_t m, uint32_t n, bool with_q);
+void qr_tsqr_one(const float* a, float* q, float* r, uint32_t m, uint32_t n, float* work, hipStream_t s);
+
 // ---- Cholesky, n <= 32 ----
 bool chol_small_fits(uint32_t n);
 void chol_small(const float* a, float* l, uint32_t* info, uint32_t batch, uint32_t n, bool upper, hipStream_t s);

@@ -109,9 +109,27 @@ void copy_block(const float* src, int lds, float* dst, int ldd, int rows, int co
 
 }  // namespace
 
+namespace {
+
+// The fix-up's QR of the tall factor (l x k): blocked to 4096 rows, a tree
+// of blocked QRs beyond
+bool tall_qr_fits(uint32_t l, uint32_t k) { return qr_blocked_fits(l, k) || qr_tsqr_fits(l, k, k); }
+
+size_t tall_qr_floats(uint32_t l, uint32_t k) {
+    const size_t tall = qr_blocked_fits(l, k) ? qr_blocked_workspace(l, k) : qr_tsqr_workspace(l, k, true);
+    return std::max(tall, qr_blocked_workspace(k, k)) / sizeof(float) + 64;
+}
+
+void tall_qr(const float* a, float* q, float* r, uint32_t l, uint32_t k, float* work, hipStream_t s) {
+    if (qr_blocked_fits(l, k)) qr_blocked(a, q, r, 1, l, k, k, k, work, s);
+    else qr_tsqr_one(a, q, r, l, k, work, s);
+}
+
+}  // namespace
+
 bool svd_large_fits(uint32_t m, uint32_t n) {
     const uint32_t l = std::max(m, n), k = std::min(m, n);
-    return k >= 1 && qr_blocked_fits(l, k) && eigh_blocked_fits(2 * k);
+    return k >= 1 && qr_blocked_fits(k, k) && tall_qr_fits(l, k) && eigh_blocked_fits(2 * k);
 }
 
 size_t svd_large_workspace(uint32_t m, uint32_t n) {
@@ -121,7 +139,7 @@ size_t svd_large_workspace(uint32_t m, uint32_t n) {
     floats += 4 * l * k + 3 * k * k + 3 * 64 * 64;   // T, U, Q, C, V, Vt', R
     floats += svd_small_workspace(64, 64, 1) / sizeof(float) + 64;
     floats += apply_reflectors_wy_floats((int)l, (int)k) + 64;
-    const size_t qw = qr_blocked_workspace((uint32_t)l, (uint32_t)k) / sizeof(float) + 64;
+    const size_t qw = tall_qr_floats((uint32_t)l, (uint32_t)k);
     return (floats + qw + 20 * 64) * sizeof(float);   // + the 64-float rounding of each piece
 }
 
@@ -153,7 +171,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     float* C = take((size_t)m * k);
     float* sws = take(svd_small_workspace(64, 64, 1) / sizeof(float) + 64);
     float* wyw = take(apply_reflectors_wy_floats(m, k));
-    float* qw = take(qr_blocked_workspace((uint32_t)m, (uint32_t)k) / sizeof(float) + 64);
+    float* qw = take(tall_qr_floats((uint32_t)m, (uint32_t)k));
     uint32_t* dinfo = reinterpret_cast<uint32_t*>(take(64));
 
     const float* tall = a;
@@ -208,7 +226,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
             copy_block(Q + g, k, V + g, k, k, nj, st);
             sgemm(false, false, m, nj, k, 1.0f, tall, k, 0, V + g, k, 0, 0.0f, C, nj, 0, 1, st);   // A V_J
             copy_block(C, nj, Ut + g, k, m, nj, st);
-            qr_blocked(Ut, Q, R, 1, (uint32_t)m, (uint32_t)k, (uint32_t)k, (uint32_t)k, qw, st);
+            tall_qr(Ut, Q, R, (uint32_t)m, (uint32_t)k, qw, st);
             copy_block(Q + g, k, Ut + g, k, m, nj, st);
             if (nj <= 64) {
                 float* Bm = R;                     // nj x nj

@@ -254,6 +254,49 @@ def test_qr_blocked_special(cuda, api, oracle):
     assert recon.max() <= bound(m) and ortho.max() <= bound(m) and dr <= 1e-4
 
 
+@pytest.mark.parametrize("m,n", [(4097, 65), (6000, 100), (20000, 130), (40000, 512)])
+def test_qr_tree_shapes(cuda, api, oracle, m, n):
+    """Past the blocked QR's 4096 rows with more than 64 columns: a tree of
+    blocked QRs (40000 x 512 stacks 5120 rows of R and takes a second
+    level).  R is compared by magnitude: its row signs are the tree's."""
+    a = gaussian((1, m, n), m + n)
+    q, r = api.qr(a, "reduced")
+    qo, ro = oracle.qr(a, "reduced")
+    q, r = to_np(q), to_np(r)
+    assert q.shape == (1, m, n) and r.shape == (1, n, n)
+    recon, ortho, dr = _qr_check(a, q, r, ro, n)
+    print(f"[qr tree {m}x{n}] recon {recon.max():.3e} ortho {ortho.max():.3e} |R| vs LAPACK {dr:.3e}")
+    assert recon.max() <= bound(m) and ortho.max() <= bound(m) and dr <= 1e-4
+    _, r2 = api.qr(a, "r")
+    assert np.array_equal(to_np(r2).view(np.uint32), r.view(np.uint32))
+
+
+def test_qr_tree_special(cuda, api, oracle):
+    m, n = 5000, 70
+    a = gaussian((4, m, n), 6)
+    a[1, 4321, 3] = np.nan
+    a[2] = 0.0
+    a[3] *= 1e30
+    q, r = api.qr(a, "reduced")
+    q, r = to_np(q), to_np(r)
+    assert np.isnan(q[1]).all() and np.isnan(r[1]).all()
+    assert np.isfinite(q[[0, 2, 3]]).all() and np.isfinite(r[[0, 2, 3]]).all()
+    assert np.array_equal(q[2], np.eye(m, n, dtype=np.float32)) and np.all(r[2] == 0)
+    qo, ro = oracle.qr(a[[0, 3]], "reduced")
+    recon, ortho, dr = _qr_check(a[[0, 3]], q[[0, 3]], r[[0, 3]], ro, n)
+    assert recon.max() <= bound(m) and ortho.max() <= bound(m) and dr <= 1e-4
+
+
+@pytest.mark.parametrize("m,n,mode", [(5000, 70, "complete"), (5000, 2049, "reduced")])
+def test_qr_tree_limits(cuda, api, m, n, mode):
+    """Complete Q past 4096 rows, and more than 2048 columns past 4096 rows:
+    an argument error naming the limits, nothing computed."""
+    a = np.zeros((1, m, n), np.float32)
+    with pytest.raises(api.MetalLinalgError) as e:
+        api.qr(a, mode)
+    assert e.value.status == 1 and "2048 columns" in str(e.value)
+
+
 def test_config5_qr(cuda, api, oracle):
     torch = cuda
     g = config5_matrix()

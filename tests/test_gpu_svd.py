@@ -161,9 +161,12 @@ def test_tall_special(cuda, api, oracle):
     assert (info[2] >> 18) & 1   # rank-deficient
 
 
-# ---- min(M, N) > 64: the large eigh path on [0 A^T; A 0] ----
+# ---- min(M, N) > 64 beyond the batched windows: bidiagonalisation, then the
+# Golub-Kahan tridiagonal's eigenpairs (5000 and 4500 rows: past 4096, the
+# fix-up's QR of U is a tree of blocked QRs) ----
 
-@pytest.mark.parametrize("m,n", [(65, 65), (100, 80), (80, 100), (300, 130), (130, 513), (1024, 1024)])
+@pytest.mark.parametrize("m,n", [(65, 65), (100, 80), (80, 100), (300, 130), (130, 513), (1024, 1024), (5000, 100),
+                                 (90, 4500)])
 def test_large(cuda, api, oracle, m, n):
     a = gaussian((1, m, n), seed=m * 3 + n)
     u, s, vt, info = api.svd(a, True)
@@ -181,6 +184,23 @@ def test_large(cuda, api, oracle, m, n):
     assert np.all(np.diff(s, axis=-1) <= 0) and np.all(s >= 0)
     _, s2, _, _ = api.svd(a, False)
     assert values_close(s2, s).max() <= 1e-5
+
+
+def test_large_tall_rank_deficient(cuda, api, oracle):
+    """5000 x 120 of rank 60: the zero cluster's columns are rebuilt from the
+    QR of U, past 4096 rows a tree of blocked QRs."""
+    rng = np.random.default_rng(47)
+    m, n = 5000, 120
+    a = (rng.standard_normal((m, 60)) @ rng.standard_normal((60, n))).astype(np.float32)[None]
+    u, s, vt, info = api.svd(a, True)
+    _, so, _, _ = oracle.svd(a, False)
+    info = u32(info)
+    recon, ou, ov = svd_residuals(a, u, s, vt)
+    close = values_close(s, so)
+    print(f"[svd large tall rank 60] recon {recon.max():.3e} orthoU {ou.max():.3e} orthoV {ov.max():.3e} "
+          f"values {close.max():.3e} info {info[0]:#x}")
+    assert recon.max() <= bound(m) and ou.max() <= bound(n) and ov.max() <= bound(n)
+    assert close.max() <= 1e-5 and (info[0] >> 18) & 1
 
 
 def test_large_special(cuda, api, oracle):
