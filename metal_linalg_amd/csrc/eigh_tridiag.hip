@@ -296,11 +296,12 @@ __global__ __launch_bounds__(64) void wy_t_kernel(const float* __restrict__ S, c
 }
 
 // out[i][j] = Z[i][perm[j]]; w[j] = lam[perm[j]] 2^e
+// V (n x cols) column j = Z (n x n) column perm[j]
 __global__ __launch_bounds__(256) void permute_columns_kernel(const float* __restrict__ Z, float* __restrict__ V,
-                                                              const int* __restrict__ perm, int n) {
+                                                              const int* __restrict__ perm, int n, int cols) {
     const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)n * n) return;
-    const int i = (int)(idx / n), j = (int)(idx - (size_t)i * n);
+    if (idx >= (size_t)n * cols) return;
+    const int i = (int)(idx / cols), j = (int)(idx - (size_t)i * cols);
     V[idx] = Z[(size_t)i * n + perm[j]];
 }
 
@@ -405,9 +406,10 @@ size_t eigh_tridiag_floats(uint32_t n) {
 // Stages 2 and 3 on one matrix after sytrd_one: w_out (n), and if v_out
 // V (n x n) with the eigenvectors as columns; info.
 void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out, uint32_t* info, hipStream_t s,
-                      bool backtransform) {
+                      bool backtransform, uint32_t il) {
     const int n = (int)nn;
     const size_t N = nn;
+    const int nw = n - (int)il;   // eigenvectors wanted: those of eigenvalues il .. n-1
     float* p = w.rest;
     auto take = [&](size_t c) {
         float* r = p;
@@ -435,7 +437,7 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
     MLA_HIP(hipStreamSynchronize(s));
     if (hflags[1]) {   // a non-finite entry: all NaN
         hipLaunchKernelGGL(fill_nan_kernel, dim3(grid_of(N)), dim3(256), 0, s, w_out, N);
-        if (v_out) hipLaunchKernelGGL(fill_nan_kernel, dim3(grid_of(N * N)), dim3(256), 0, s, v_out, N * N);
+        if (v_out) hipLaunchKernelGGL(fill_nan_kernel, dim3(grid_of(N * nw)), dim3(256), 0, s, v_out, N * nw);
         MLA_HIP(hipGetLastError());
         return;
     }
@@ -495,7 +497,11 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
         return;
     }
 
-    // clusters: consecutive eigenvalues of a block within 1e-5 ||T||
+    // clusters: consecutive eigenvalues of a block within 1e-5 ||T||; only
+    // those holding a wanted eigenvalue (rank il or above) are solved, each
+    // whole (its members are orthogonalised together)
+    std::vector<int> rank(N);
+    for (int r = 0; r < n; ++r) rank[hp[r]] = r;
     std::vector<Cluster> hc;
     const float ctol = 1e-5f * tnorm;
     for (size_t b = 0; b + 1 < bstart.size(); ++b) {
@@ -504,7 +510,9 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
         while (k < m) {
             int c = 1;
             while (k + c < m && hl[s0 + k + c] - hl[s0 + k + c - 1] <= ctol) ++c;
-            hc.push_back(Cluster{s0, m, s0 + k, c});
+            bool want = false;
+            for (int q = 0; q < c; ++q) want |= rank[s0 + k + q] >= (int)il;
+            if (want) hc.push_back(Cluster{s0, m, s0 + k, c});
             k += c;
         }
     }
@@ -514,14 +522,19 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
     float* U = scratch;
     {
         KernelTimer tm("tridiag_vectors", s);
-        hipLaunchKernelGGL(inverse_iteration_kernel, dim3((unsigned)cdiv(ncl, 64)), dim3(64), 0, s, w.d, dE,
-                           clusters, ncl, lam, tnorm, Z, n, n, U);
-        // Z <- Z (3 I - Z^T Z) / 2
-        float* G = scratch;
-        sgemm(true, false, n, n, n, 1.0f, Z, n, 0, Z, n, 0, 0.0f, G, n, 0, 1, s);
-        hipLaunchKernelGGL(newton_schulz_kernel, dim3((unsigned)cdiv(N * N, 256)), dim3(256), 0, s, G, n);
-        sgemm(false, false, n, n, n, 1.0f, Z, n, 0, G, n, 0, 0.0f, v_out, n, 0, 1, s);
-        MLA_HIP(hipMemcpyAsync(Z, v_out, N * N * sizeof(float), hipMemcpyDeviceToDevice, s));
+        if (ncl > 0)
+            hipLaunchKernelGGL(inverse_iteration_kernel, dim3((unsigned)cdiv(ncl, 64)), dim3(64), 0, s, w.d, dE,
+                               clusters, ncl, lam, tnorm, Z, n, n, U);
+        // the wanted columns in ascending order, Zs = Z[:, perm[il ..]]
+        // (n x nw), then one Newton-Schulz step Zs <- Zs (3 I - Zs^T Zs) / 2
+        // into v_out
+        float* Zs = scratch;
+        float* G = scratch + N * nw;
+        hipLaunchKernelGGL(permute_columns_kernel, dim3((unsigned)cdiv(N * nw, 256)), dim3(256), 0, s, Z, Zs,
+                           perm + il, n, nw);
+        sgemm(true, false, nw, nw, n, 1.0f, Zs, nw, 0, Zs, nw, 0, 0.0f, G, nw, 0, 1, s);
+        hipLaunchKernelGGL(newton_schulz_kernel, dim3((unsigned)cdiv((size_t)nw * nw, 256)), dim3(256), 0, s, G, nw);
+        sgemm(false, false, n, nw, nw, 1.0f, Zs, nw, 0, G, nw, 0, 0.0f, v_out, nw, 0, 1, s);
         tm.stop();
     }
     // V = Q Z: panels from the last, Z2 = Z[j0 + 1 :, :] -= V (T (V^T Z2))
@@ -529,10 +542,9 @@ void eigh_tridiag_one(const EighWork& w, uint32_t nn, float* w_out, float* v_out
     // operands stay 16-byte aligned)
     if (backtransform) {
         KernelTimer tm("eigh_backtransform", s);
-        apply_reflectors_wy(w.V, n, w.tau, n - 1, n, Z, n, part, s);
+        apply_reflectors_wy(w.V, n, w.tau, n - 1, n, v_out, nw, part, s);
         tm.stop();
     }
-    hipLaunchKernelGGL(permute_columns_kernel, dim3((unsigned)cdiv(N * N, 256)), dim3(256), 0, s, Z, v_out, perm, n);
     MLA_HIP(hipStreamSynchronize(s));   // the host vectors above must outlive the copies
     MLA_HIP(hipGetLastError());
 }

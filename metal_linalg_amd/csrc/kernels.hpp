@@ -98,11 +98,12 @@ EighWork eigh_carve(float* base, uint32_t n);
 void sytrd_one(const float* a, uint32_t n, bool lower, const EighWork& w, hipStream_t s);
 // y = x * 2^e (the scale stage 1 took out), or NaN for a non-finite matrix
 void eigh_unscale(const float* x, float* y, uint32_t count, const uint32_t* flags, hipStream_t s);
-// stages 2 and 3 after sytrd_one: eigenvalues (ascending), eigenvectors if
-// v_out, info; the workspace after stage 1's holds eigh_tridiag_floats(n)
+// stages 2 and 3 after sytrd_one: eigenvalues (ascending, all n), the
+// eigenvectors of eigenvalues il .. n-1 if v_out (n x (n - il), ascending),
+// info; the workspace after stage 1's holds eigh_tridiag_floats(n)
 size_t eigh_tridiag_floats(uint32_t n);
 void eigh_tridiag_one(const EighWork& w, uint32_t n, float* w_out, float* v_out, uint32_t* info, hipStream_t s,
-                      bool backtransform = true);
+                      bool backtransform = true, uint32_t il = 0);
 // Z (rows x cols, row-major) <- H_0 H_1 ... H_{nrefl-1} Z with H_j = I -
 // tau_j v_j v_j^T, v_j row j of V (stride ldv, zero before its leading 1),
 // in compact-WY panels on the MFMA GEMM; work = apply_reflectors_wy_floats.

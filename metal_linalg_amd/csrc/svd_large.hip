@@ -35,10 +35,10 @@
 namespace mla {
 namespace {
 
-// From the Golub-Kahan tridiagonal's eigenpairs (ascending w, Z 2k x 2k):
-// s_i = max(w[2k-1-i], 0) (NaN kept); U[r][i] = sqrt2 Z[2r+1][2k-1-i] for r < k (rows
-// k .. m-1 of U zero: Q's reflectors fill them); V[c][i] (as Vt[i][c]) =
-// sqrt2 Z[2c][2k-1-i]
+// From the Golub-Kahan tridiagonal's eigenpairs (w ascending, all 2k; Z
+// 2k x k, the eigenvectors of w[k .. 2k-1]): s_i = max(w[2k-1-i], 0) (NaN
+// kept); U[r][i] = sqrt2 Z[2r+1][k-1-i] for r < k (rows k .. m-1 of U zero:
+// Q's reflectors fill them); V[c][i] (as Vt[i][c]) = sqrt2 Z[2c][k-1-i]
 __global__ __launch_bounds__(256) void tgk_extract_kernel(const float* __restrict__ Z, const float* __restrict__ w,
                                                           int m, int k, float* __restrict__ U, float* __restrict__ Vt,
                                                           float* __restrict__ s) {
@@ -50,13 +50,15 @@ __global__ __launch_bounds__(256) void tgk_extract_kernel(const float* __restric
         s[idx] = x != x ? x : fmaxf(x, 0.0f);   // a NaN (non-finite input) stays NaN
     }
     if (Z == nullptr) return;
+    // Z (2k x k) holds the eigenvectors of w[k .. 2k-1], ascending: that of
+    // s_i = w[2k-1-i] is column k-1-i
     if (U && idx < (size_t)m * k) {
         const int r = (int)(idx / k), i = (int)(idx - (size_t)r * k);
-        U[idx] = r < k ? sq2 * Z[(size_t)(2 * r + 1) * n2 + (n2 - 1 - i)] : 0.0f;
+        U[idx] = r < k ? sq2 * Z[(size_t)(2 * r + 1) * k + (k - 1 - i)] : 0.0f;
     }
     if (idx < (size_t)k * k) {
         const int i = (int)(idx / k), c = (int)(idx - (size_t)i * k);
-        Vt[idx] = sq2 * Z[(size_t)(2 * c) * n2 + (n2 - 1 - i)];
+        Vt[idx] = sq2 * Z[(size_t)(2 * c) * k + (k - 1 - i)];
     }
 }
 
@@ -135,7 +137,7 @@ bool svd_large_fits(uint32_t m, uint32_t n) {
 size_t svd_large_workspace(uint32_t m, uint32_t n) {
     const size_t l = std::max(m, n), k = std::min(m, n), n2 = 2 * k;
     size_t floats = bidiag_floats((uint32_t)l, (uint32_t)k) + eigh_tridiag_floats((uint32_t)n2);
-    floats += 2 * n2 + n2 * n2 + n2 + 64;            // the tridiagonal, Z, w
+    floats += 2 * n2 + n2 * k + n2 + 64;             // the tridiagonal, Z, w
     floats += 4 * l * k + 3 * k * k + 3 * 64 * 64;   // T, U, Q, C, V, Vt', R
     floats += svd_small_workspace(64, 64, 1) / sizeof(float) + 64;
     floats += apply_reflectors_wy_floats((int)l, (int)k) + 64;
@@ -160,7 +162,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     ew.e = take((size_t)n2);
     ew.flags = bd.flags;
     ew.rest = take(eigh_tridiag_floats((uint32_t)n2));
-    float* Z = vec ? take((size_t)n2 * n2) : nullptr;
+    float* Z = vec ? take((size_t)n2 * k) : nullptr;
     float* w = take((size_t)n2);
     float* T = take((size_t)m * k);
     float* Ut = take((size_t)m * k);    // the tall problem's U (m x k)
@@ -181,7 +183,7 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     }
     bidiag_one(tall, (uint32_t)m, (uint32_t)k, bd, st);
     tgk_build(bd, (uint32_t)k, ew.d, ew.e, st);
-    eigh_tridiag_one(ew, (uint32_t)n2, w, Z, dinfo, st, false);
+    eigh_tridiag_one(ew, (uint32_t)n2, w, Z, dinfo, st, false, (uint32_t)k);   // the k eigenvectors of +s
     hipLaunchKernelGGL(tgk_extract_kernel, dim3(blocks(std::max((size_t)m * k, (size_t)k * k))), dim3(256), 0, st, Z,
                        w, m, k, vec ? Ut : nullptr, Vtt, s);
 
