@@ -10,16 +10,16 @@
 //
 // Working layout: T's columns contiguous (column-major copy scaled by a
 // power of two into [0.5, 1)), so that a column is a coalesced vector and a
-// product A v walks rows across the threads.  Per column j, four launches:
+// product A v walks rows across the threads.  Per column j, three launches:
 //   bd_col      one workgroup: column j (with the previous step's right
 //               update applied) -> the left reflector u_j (kept as row j of
 //               VL), tau_q, d_j
 //   bd_left     a workgroup per trailing column, held in registers: the
 //               previous right update, then H_j; row j's entries after H_j
 //               go to rowbuf
-//   bd_row      one workgroup: the right reflector v_j from rowbuf (row j of
-//               VR, leading 1 at j + 1), tau_p, e_j
-//   bd_matvec   x = A v_j over rows j+1 .. m-1 (a workgroup per 32-row
+//   bd_matvec   the right reflector v_j from rowbuf (every workgroup forms
+//               it; the first records it as row j of VR with tau_p, e_j),
+//               then x = A v_j over rows j+1 .. m-1 (a workgroup per 32-row
 //               tile, all columns); the update A -= tau_p x v_j^T is folded
 //               into the next column's bd_col and bd_left, which read every
 //               entry anyway
@@ -207,49 +207,52 @@ __global__ __launch_bounds__(256) void bd_left_long_kernel(float* __restrict__ A
     }
 }
 
-// The right reflector from rowbuf[j+1 .. k-1] (row j of the left-updated
-// matrix): v_j with its leading 1 at j + 1, tau_p, e_j.
-__global__ __launch_bounds__(kColThreads) void bd_row_kernel(const float* __restrict__ rowbuf, int k, int j,
-                                                             float* __restrict__ VR, float* __restrict__ taup,
-                                                             float* __restrict__ e) {
-    __shared__ float red[kColThreads / 64];
-    const int t = threadIdx.x;
-    float ss = 0.0f;
-    for (int c = j + 2 + t; c < k; c += kColThreads) ss = fmaf(rowbuf[c], rowbuf[c], ss);
-    ss = block_sum_1024(ss, red);
-    const float alpha = rowbuf[j + 1];
-    float beta = alpha, tau = 0.0f, scale = 1.0f;
-    if (ss >= kTinySumsq) {
-        beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
-        tau = (beta - alpha) / beta;
-        scale = 1.0f / (alpha - beta);
-    }
-    float* v = VR + (size_t)j * k;
-    for (int c = t; c < k; c += kColThreads) v[c] = c <= j ? 0.0f : (c == j + 1 ? 1.0f : rowbuf[c] * scale);
-    if (t == 0) {
-        taup[j] = tau;
-        e[j] = beta;
-    }
-}
-
-// x[r] = sum_{c > j} A[r][c] v_j[c] for rows r = j+1 .. m-1, in one pass:
-// a 1024-thread workgroup per tile of 32 rows from r0 = (j + 1) & ~3 (rows
-// below j + 1 come along and are dropped; the pad rows are zero).  A lane
-// holds 4 rows (16-byte loads): 8 lanes cover the tile, and the 128 column
-// lanes of the workgroup take every 128th column, kMvBatch loads in flight
-// before the first product; the 128 sums per row meet in LDS in a fixed
-// order.  (Splitting the columns over workgroups instead needs a
-// device-scope fence per workgroup to combine them, which costs more than
-// the product on this chip.)
-__global__ __launch_bounds__(1024) void bd_matvec_kernel(const float* __restrict__ Ac, int m, int ld, int k, int j,
-                                                         const float* __restrict__ VR, float* __restrict__ x) {
+// The right reflector v_j from rowbuf[j+1 .. k-1] (row j of the
+// left-updated matrix; its leading 1 at j + 1), then x[r] = sum_{c > j}
+// A[r][c] v_j[c] for rows r = j+1 .. m-1.  Every workgroup forms v_j (the
+// same sum of squares in the same order, so the same bits) and workgroup 0
+// records it (row j of VR, tau_p, e_j), which saves a launch per column.
+// The product in one pass: a 1024-thread workgroup per tile of 32 rows from
+// r0 = (j + 1) & ~3 (rows below j + 1 come along and are dropped; the pad
+// rows are zero).  A lane holds 4 rows (16-byte loads): 8 lanes cover the
+// tile, and the 128 column lanes of the workgroup take every 128th column,
+// kMvBatch loads in flight before the first product; the 128 sums per row
+// meet in LDS in a fixed order.  (Splitting the columns over workgroups
+// instead needs a device-scope fence per workgroup to combine them, which
+// costs more than the product on this chip.)
+__global__ __launch_bounds__(kColThreads) void bd_matvec_kernel(const float* __restrict__ Ac, int m, int ld, int k,
+                                                                int j, const float* __restrict__ rowbuf,
+                                                                float* __restrict__ VR, float* __restrict__ taup,
+                                                                float* __restrict__ e, float* __restrict__ x) {
     __shared__ float red[128][33];
     __shared__ float red2[32][33];
+    __shared__ float rsum[kColThreads / 64];
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    float scale;
+    {
+        float ss = 0.0f;
+        for (int c = j + 2 + t; c < k; c += kColThreads) ss = fmaf(rowbuf[c], rowbuf[c], ss);
+        ss = block_sum_1024(ss, rsum);
+        const float alpha = rowbuf[j + 1];
+        float beta = alpha, tau = 0.0f;
+        scale = 1.0f;
+        if (ss >= kTinySumsq) {
+            beta = -copysignf(sqrtf(fmaf(alpha, alpha, ss)), alpha);
+            tau = (beta - alpha) / beta;
+            scale = 1.0f / (alpha - beta);
+        }
+        if (blockIdx.x == 0) {
+            float* v = VR + (size_t)j * k;
+            for (int c = t; c < k; c += kColThreads) v[c] = c <= j ? 0.0f : (c == j + 1 ? 1.0f : rowbuf[c] * scale);
+            if (t == 0) {
+                taup[j] = tau;
+                e[j] = beta;
+            }
+        }
+    }
     const int rl = l & 7, cl = (w << 3) | (l >> 3);
     const int r0 = ((j + 1) & ~3) + blockIdx.x * 32;
     const int rq = min(r0 + 4 * rl, ld - 4);   // in the allocation; rows beyond m are dropped below
-    const float* v = VR + (size_t)j * k;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int cb = j + 1 + cl; cb < k; cb += 128 * kMvBatch) {
         float4 av[kMvBatch];
@@ -259,7 +262,7 @@ __global__ __launch_bounds__(1024) void bd_matvec_kernel(const float* __restrict
             const int c = cb + 128 * i;
             const int cc = min(c, k - 1);
             av[i] = *reinterpret_cast<const float4*>(Ac + (size_t)cc * ld + rq);
-            vv[i] = v[cc] * (c < k ? 1.0f : 0.0f);
+            vv[i] = (cc == j + 1 ? 1.0f : rowbuf[cc] * scale) * (c < k ? 1.0f : 0.0f);
         }
 #pragma unroll
         for (int i = 0; i < kMvBatch; ++i) {
@@ -353,11 +356,10 @@ void bidiag_one(const float* T, uint32_t mm, uint32_t kk, const Bidiag& b, hipSt
             hipLaunchKernelGGL(bd_left_long_kernel, dim3((unsigned)cdiv(cols, 4)), dim3(256), 0, s, b.Ac, m, ld, k, j,
                                b.x, b.taup, b.VR, b.VL, b.tauq, b.rowbuf);
 #undef MLA_BD_LEFT
-        hipLaunchKernelGGL(bd_row_kernel, dim3(1), dim3(kColThreads), 0, s, b.rowbuf, k, j, b.VR, b.taup, b.e);
         // rows j+1 .. m-1 (m > j + 1 since m >= k > j + 1)
         const int r0 = (j + 1) & ~3;
-        hipLaunchKernelGGL(bd_matvec_kernel, dim3((unsigned)cdiv(m - r0, 32)), dim3(1024), 0, s, b.Ac, m, ld, k, j,
-                           b.VR, b.x);
+        hipLaunchKernelGGL(bd_matvec_kernel, dim3((unsigned)cdiv(m - r0, 32)), dim3(kColThreads), 0, s, b.Ac, m, ld,
+                           k, j, b.rowbuf, b.VR, b.taup, b.e, b.x);
     }
     t.stop();
     MLA_HIP(hipGetLastError());
