@@ -66,13 +66,43 @@ __global__ __launch_bounds__(256) void tgk_extract_kernel(const float* __restric
 // eigenvector of the tridiagonal can carry a little of its -s partner, which moves weight
 // between its u and v parts without turning either.  One thread per column;
 // the loop walks rows, so a wave reads consecutive columns of one row.
-__global__ __launch_bounds__(256) void normalize_cols_kernel(float* __restrict__ X, int rows, int cols) {
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= cols) return;
-    float ss = 0.0f;
-    for (int r = 0; r < rows; ++r) ss = fmaf(X[(size_t)r * cols + c], X[(size_t)r * cols + c], ss);
-    const float inv = ss > 0.0f ? 1.0f / sqrtf(ss) : 0.0f;
-    for (int r = 0; r < rows; ++r) X[(size_t)r * cols + c] *= inv;
+// Columns of X (rows x cols, row-major) to unit length (a zero column stays
+// zero): a 1024-thread workgroup per 64 columns, 16 row groups of 64 lanes
+// (each row of the group read coalesced), the groups' sums of squares added
+// in LDS in a fixed order.
+__global__ __launch_bounds__(1024) void normalize_cols_kernel(float* __restrict__ X, int rows, int cols) {
+    __shared__ float part[16][64];
+    __shared__ float inv_s[64];
+    const int t = threadIdx.x, cl = t & 63, rg = t >> 6;
+    const int c = blockIdx.x * 64 + cl;
+    const bool live = c < cols;
+    const int cc = live ? c : 0;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    int r = rg;
+    for (; r + 48 < rows; r += 64) {
+        const float a = X[(size_t)r * cols + cc], b = X[(size_t)(r + 16) * cols + cc];
+        const float d = X[(size_t)(r + 32) * cols + cc], e = X[(size_t)(r + 48) * cols + cc];
+        s0 = fmaf(a, a, s0);
+        s1 = fmaf(b, b, s1);
+        s2 = fmaf(d, d, s2);
+        s3 = fmaf(e, e, s3);
+    }
+    for (; r < rows; r += 16) {
+        const float a = X[(size_t)r * cols + cc];
+        s0 = fmaf(a, a, s0);
+    }
+    part[rg][cl] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (rg == 0) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) ss += part[g][cl];
+        inv_s[cl] = ss > 0.0f ? 1.0f / sqrtf(ss) : 0.0f;
+    }
+    __syncthreads();
+    if (!live) return;
+    const float inv = inv_s[cl];
+    for (int rr = rg; rr < rows; rr += 16) X[(size_t)rr * cols + c] *= inv;
 }
 
 // dst[r][c] = src[r][c] for a rows x cols block (row strides lds, ldd)
@@ -190,9 +220,10 @@ void svd_large_one(const float* a, float* u, float* s, float* vt, uint32_t* info
     if (vec) {
         // B's vectors to unit length (an eigenvector of the tridiagonal can
         // carry a little of its -s partner), then U = Q U_B, V = P V_B
-        hipLaunchKernelGGL(normalize_cols_kernel, dim3(blocks((size_t)k)), dim3(256), 0, st, Ut, m, k);
+        // (U's rows k .. m-1 are still zero: its first k rows hold the norms)
+        hipLaunchKernelGGL(normalize_cols_kernel, dim3((unsigned)cdiv(k, 64)), dim3(1024), 0, st, Ut, k, k);
         transpose_full(Vtt, V, k, k, st);
-        hipLaunchKernelGGL(normalize_cols_kernel, dim3(blocks((size_t)k)), dim3(256), 0, st, V, k, k);
+        hipLaunchKernelGGL(normalize_cols_kernel, dim3((unsigned)cdiv(k, 64)), dim3(1024), 0, st, V, k, k);
         apply_reflectors_wy(bd.VL, m, bd.tauq, k, m, Ut, k, wyw, st);
         apply_reflectors_wy(bd.VR, k, bd.taup, k - 1, k, V, k, wyw, st);
     }
