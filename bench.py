@@ -214,6 +214,14 @@ def workloads():
             tb * (2 * tm * tn * 4 + tn * tn * 4), tb * tall_flops(tm, tn), "hbm",
             lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": tb, "rows": tm, "cols": tn})
 
+    # the batched mid-size QR (m, n <= 128, a workgroup of two waves per
+    # matrix): the reference's batched QR past 64 columns
+    w["qr128"] = Workload(
+        "qr128", "qr_with_mode reduced, 4096 x 128x128 fp32 N(0,1) (the batched mid-size QR window)", 4096,
+        tall_make(4096, 128, 128, 131), lambda api, t: api.qr(t["a"], "reduced"), "qr_mid",
+        4096 * 3 * 128 * 128 * 4, 4096 * tall_flops(128, 128), "hbm",
+        lambda o, h, n: o.qr(h["a"][:n], "reduced"), {"batch": 4096, "rows": 128, "cols": 128})
+
     # the batched mid-size eigh (65 <= n <= 128, a workgroup of two waves
     # per matrix): the reference's eigh_ql window past 64
     def sym_make(batch, n, seed):

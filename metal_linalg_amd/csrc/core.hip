@@ -66,9 +66,11 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
     // tall matrices of at most 64 columns: the batched tall kernel (a tree
     // of 128-row blocks past 128 rows)
     const bool tall = !small && qr_tall_fits(M, N, QC);
+    // up to 128 rows and columns (one of them above 64): two waves a matrix
+    const bool mid = !small && !tall && qr_mid_fits(M, N, QC);
     // beyond the blocked QR's 4096 rows: a tree of blocked QRs, to 2048 columns
-    const bool tree = !small && !tall && !qr_blocked_fits(M, N) && qr_tsqr_fits(M, N, QC);
-    if (!small && !tall && !tree && !qr_blocked_fits(M, N))
+    const bool tree = !small && !tall && !mid && !qr_blocked_fits(M, N) && qr_tsqr_fits(M, N, QC);
+    if (!small && !tall && !mid && !tree && !qr_blocked_fits(M, N))
         invalid("[qr] " + std::to_string(M) + "x" + std::to_string(N) + (mode == QrMode::complete ? " complete" : "") +
                 ": this build's QR kernels take at most 4096 rows beyond 64 columns, or any number of rows "
                 "with at most 2048 columns (reduced or R only)");
@@ -84,7 +86,7 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
         call.finish();
         return;
     }
-    if (small || tall) {
+    if (small || tall || mid) {
         const std::vector<Call::Slice> sl = {{a.data, nullptr, (size_t)M * N * 4},
                                              {nullptr, QC ? q : nullptr, (size_t)M * QC * 4},
                                              {nullptr, r, (size_t)RR * N * 4}};
@@ -92,7 +94,8 @@ void qr(const Matrices& a, float* q, float* r, QrMode mode) {
         float* ws = wsb ? static_cast<float*>(call.scratch(wsb)) : nullptr;
         call.batched(B, sl, [&](void* const* d, uint32_t nb, hipStream_t s) {
             if (small) qr_small(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, QC, RR, s);
-            else qr_tall(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, ws, s);
+            else if (tall) qr_tall(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, ws, s);
+            else qr_mid(f32(d[0]), f32(d[1]), f32(d[2]), nb, M, N, s);
         });
         call.finish();
         return;

@@ -24,6 +24,11 @@ size_t qr_tall_workspace(uint32_t m, uint32_t n, uint32_t batch, bool with_q);
 void qr_tall(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, float* work,
              hipStream_t s);
 
+// ---- QR of the mid-size window: m, n <= 128 (one above 64), batched ----
+// Reduced mode (q [batch, m, min(m, n)]) or R alone (q NULL); r [batch, min(m, n), n].
+bool qr_mid_fits(uint32_t m, uint32_t n, uint32_t qc);
+void qr_mid(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, hipStream_t s);
+
 // ---- QR for larger matrices (m <= 4096), one matrix at a time ----
 // work = qr_blocked_workspace(m, n) bytes; q may be NULL when qc = 0.
 bool qr_blocked_fits(uint32_t m, uint32_t n);

@@ -387,6 +387,141 @@ void launch_level(const float* x, float* q, float* r, uint32_t cnt, const Level&
 // Matrices per launch so that a launch stays within kMaxGrid workgroups.
 uint64_t mats_per_launch(const Level& l) { return std::max<uint64_t>(1, kMaxGrid / (uint64_t)l.blocks); }
 
+// ---- the mid-size window: up to 128 rows and 128 columns, two waves ----
+//
+// qr_mid_kernel: the same steps over a workgroup of two waves, thread c
+// owning column c (c < n <= 128), rows in VGPRs (m <= 16 MC <= 128).  Step
+// J's reflector is formed by thread J alone from its own column and
+// published in LDS (u, coef, u_J, beta) before the step's one barrier: the
+// other wave cannot read lane J's registers.  K = min(m, n) steps (a wide
+// matrix's later columns only take the updates); Q is m x K (reduced, or R
+// alone), R is K x n.
+constexpr int kMidCols = 128;
+
+template <int P, int MC>
+__device__ __forceinline__ void mid_factor_step(float (&x)[MC * kChunk], float* u, float* csh, float* ujsh,
+                                                float* bsh, int c, int J) {
+    constexpr int R0 = P * kChunk, RE = MC * kChunk;
+    int cl = c;
+    __asm__ volatile("" : "+v"(cl));
+    if (cl == J) {
+        float al = 0.0f, s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const int r = R0 + i;
+            al = r == J ? x[r] : al;
+            s0 = fmaf(r > J ? x[r] : 0.0f, x[r], s0);
+        }
+#pragma unroll
+        for (int r = R0 + kChunk; r < RE; r += 2) {
+            s0 = fmaf(x[r], x[r], s0);
+            s1 = fmaf(x[r + 1], x[r + 1], s1);
+        }
+        const float ss = s0 + s1;
+        const bool nz = ss >= kTinySumsq;
+        const float b = -copysignf(__builtin_amdgcn_sqrtf(fmaf(al, al, ss)), al);
+        const float uj = nz ? al - b : 1.0f;
+        float v[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const int r = R0 + i;
+            v[i] = r < J ? 0.0f : (r == J ? uj : x[r]);
+        }
+        write_chunk(u + R0, v);
+#pragma unroll
+        for (int r = R0 + kChunk; r < RE; r += 4)
+            *reinterpret_cast<float4*>(u + r) = make_float4(x[r], x[r + 1], x[r + 2], x[r + 3]);
+        csh[J] = nz ? rcp_refined(b * (b - al)) : 0.0f;
+        ujsh[J] = uj;
+        bsh[J] = nz ? b : al;
+    }
+    __syncthreads();
+    const float right = cl > J ? 1.0f : 0.0f;
+    const float d = csh[J] * dot_u<R0, RE>(u, x) * right;
+    axpy_u<R0, RE, false>(x, u, d, J, 0.0f);
+}
+
+template <int P, int MC>
+__device__ __forceinline__ void mid_factor_phases(float (&x)[MC * kChunk], float* ush, float* csh, float* ujsh,
+                                                  float* bsh, int c, int K) {
+    if constexpr (P < MC) {
+        const int je = min(P * kChunk + kChunk, K);
+        for (int J = P * kChunk; J < je; ++J)
+            mid_factor_step<P, MC>(x, ush + (J & 1) * kTallRows, csh, ujsh, bsh, c, J);
+        mid_factor_phases<P + 1, MC>(x, ush, csh, ujsh, bsh, c, K);
+    }
+}
+
+template <int MC>
+__global__ __launch_bounds__(kMidCols) void qr_mid_kernel(const float* __restrict__ A, float* __restrict__ Q,
+                                                          float* __restrict__ R, uint32_t batch, int m, int n) {
+    constexpr int RE = MC * kChunk;
+    __shared__ __align__(16) float ush[2 * kTallRows];
+    __shared__ float csh[kMidCols], ujsh[kMidCols], bsh[kMidCols];
+    __shared__ float red[2];
+    __shared__ int redb[2];
+    const uint32_t mat = blockIdx.x;
+    if (mat >= batch) return;
+    const int c = threadIdx.x, lane = c & 63, wv = c >> 6;
+    const int K = min(m, n);
+    const bool col = c < n;
+    const float* src = A + (size_t)mat * m * n + (col ? c : 0);
+    const float keep = col ? 1.0f : 0.0f;
+    // every thread loads (clamped: threads past n read column 0, rows past m
+    // row m - 1) and multiplies by 0 or 1, as in the tall kernel
+    float x[RE];
+#pragma unroll
+    for (int r = 0; r < RE; ++r) {
+        x[r] = src[(size_t)(r < m ? r : m - 1) * n] * (r < m ? keep : 0.0f);
+        if ((r & 31) == 31) __builtin_amdgcn_sched_barrier(0);
+    }
+    float amax = 0.0f;
+    int bad = 0;
+#pragma unroll
+    for (int r = 0; r < RE; ++r) {
+        amax = fmaxf(amax, fabsf(x[r]));
+        bad |= !finite_f(x[r]);
+    }
+    amax = group_max<64>(amax);
+    bad = group_or<64>(bad);
+    if (lane == 0) {
+        red[wv] = amax;
+        redb[wv] = bad;
+    }
+    __syncthreads();
+    amax = fmaxf(red[0], red[1]);
+    bad = redb[0] | redb[1];
+    const int e = bad ? 0 : scale_exponent(amax);
+#pragma unroll
+    for (int r = 0; r < RE; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
+
+    mid_factor_phases<0, MC>(x, ush, csh, ujsh, bsh, c, K);
+
+    // R (K x n): above the diagonal from the threads, the diagonal from beta
+    if (col) {
+        float* out_r = R + (size_t)mat * K * n;
+        const float unscale = ldexpf(1.0f, e);
+        const float diag = c < K ? bsh[c] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < RE; ++r)
+            if (r < K) out_r[(size_t)r * n + c] = bad ? qnan() : (r < c ? x[r] : (r == c ? diag : 0.0f)) * unscale;
+    }
+    if (!Q) return;
+    // Q (m x K) backwards from the reflectors: thread c < K holds u_c
+    {
+        const float ujc = c < K ? ujsh[c] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < RE; ++r) x[r] = c < K ? (r < c ? 0.0f : (r == c ? ujc : x[r])) : 0.0f;
+    }
+    q_phases<MC - 1, MC>(x, ush, csh, ujsh, c, K);
+    if (c < K) {
+        float* out_q = Q + (size_t)mat * m * K + c;
+#pragma unroll
+        for (int r = 0; r < RE; ++r)
+            if (r < m) out_q[(size_t)r * K] = bad ? qnan() : x[r];
+    }
+}
+
 }  // namespace
 
 bool qr_tall_fits(uint32_t m, uint32_t n, uint32_t qc) {
@@ -399,6 +534,40 @@ size_t qr_tall_workspace(uint32_t m, uint32_t n, uint32_t batch, bool with_q) {
     // level l's R factors (level l+1's matrix) and level l+1's Q
     for (size_t l = 0; l + 1 < lv.size(); ++l) floats += (size_t)batch * lv[l + 1].H * n * (with_q ? 2 : 1);
     return floats * sizeof(float);
+}
+
+bool qr_mid_fits(uint32_t m, uint32_t n, uint32_t qc) {
+    const uint32_t K = std::min(m, n);
+    return m >= 1 && n >= 1 && m <= (uint32_t)kMidCols && n <= (uint32_t)kMidCols && std::max(m, n) > 64 &&
+           (qc == 0 || qc == K);
+}
+
+void qr_mid(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, hipStream_t s) {
+    if (!qr_mid_fits(m, n, q ? std::min(m, n) : 0)) invalid("[qr] qr_mid takes m, n <= 128");
+    if (batch == 0) return;
+    KernelTimer t("qr_mid", s);
+    const int mc = (int)cdiv(m, kChunk);
+    for (uint64_t b0 = 0; b0 < batch; b0 += kMaxGrid) {
+        const uint32_t nb = (uint32_t)std::min<uint64_t>(kMaxGrid, batch - b0);
+        const float* ab = a + b0 * m * n;
+        float* qb = q ? q + b0 * m * std::min(m, n) : nullptr;
+        float* rb = r + b0 * std::min(m, n) * n;
+#define MLA_QR_MID(MC)                                                                                         \
+    hipLaunchKernelGGL(qr_mid_kernel<MC>, dim3(nb), dim3(kMidCols), 0, s, ab, qb, rb, nb, (int)m, (int)n)
+        switch (mc) {
+            case 1: MLA_QR_MID(1); break;
+            case 2: MLA_QR_MID(2); break;
+            case 3: MLA_QR_MID(3); break;
+            case 4: MLA_QR_MID(4); break;
+            case 5: MLA_QR_MID(5); break;
+            case 6: MLA_QR_MID(6); break;
+            case 7: MLA_QR_MID(7); break;
+            default: MLA_QR_MID(8); break;
+        }
+#undef MLA_QR_MID
+    }
+    t.stop();
+    MLA_HIP(hipGetLastError());
 }
 
 void qr_tall(const float* a, float* q, float* r, uint32_t batch, uint32_t m, uint32_t n, float* work,
