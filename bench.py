@@ -50,6 +50,7 @@ TRAFFIC_BYTES = {
     "qr4096x64": 2_627_819_140, # profiles/qr_tall_qr4096x64.md
     "eigh128": 2_753_827_916, # profiles/eigh_mid_eigh128.md
     "svd128": 807_681_288, # profiles/svd_jacobi_svd128.md
+    "qr128": 812_645_786, # profiles/qr_mid_qr128.md
 }
 
 # The batched kernels are bound by instruction issue, not HBM: VALU
@@ -63,6 +64,7 @@ VALU_INSTRUCTIONS = {
     "qr128x64": 388_014_080,
     "eigh128": 830_838_762,
     "svd128": 9_048_489_876,
+    "qr128": 488_611_840,
 }
 SIMDS, CLOCK_HZ = 1024, 2.4e9
 
