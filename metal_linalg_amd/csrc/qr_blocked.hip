@@ -521,12 +521,19 @@ int gram(const float* X, const float* Y, int ld, int M, int N, int K, float* par
     return nsplit;
 }
 
-// out[i] = sum_b part[b][i]
+// out[i] = sum_b part[b][i], in order of b; eight partials in flight at a
+// time (indices past the last read it again and add zero)
 __global__ __launch_bounds__(256) void sum_parts_kernel(const float* __restrict__ part, int nsplit, size_t count,
                                                         float* __restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (size_t)gridDim.x * 256) {
         float s = 0.0f;
-        for (int b = 0; b < nsplit; ++b) s += part[(size_t)b * count + i];
+        for (int b0 = 0; b0 < nsplit; b0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = part[(size_t)min(b0 + j, nsplit - 1) * count + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += v[j] * (b0 + j < nsplit ? 1.0f : 0.0f);
+        }
         out[i] = s;
     }
 }
@@ -564,15 +571,12 @@ unsigned grid_for(size_t count) { return (unsigned)std::min<size_t>(cdiv(count, 
 // ldb, or with tb B stored N x K).  Returns the number of parts.
 int split_k_gemm(bool tb, int M, int N, int K, const float* A, int lda, const float* B, int ldb, float* part,
                  hipStream_t s) {
-    const int full = K / kChunk, rest = K - full * kChunk;
+    // one batched launch, the last chunk shorter
+    const int nsplit = cdiv(K, kChunk), last = K - (nsplit - 1) * kChunk;
     const long long sb = tb ? kChunk : (long long)kChunk * ldb;
-    if (full > 0)
-        sgemm(false, tb, M, N, kChunk, 1.0f, A, lda, kChunk, B, ldb, sb, 0.0f, part, N, (long long)M * N, full, s);
-    if (rest > 0)
-        sgemm(false, tb, M, N, rest, 1.0f, A + (size_t)full * kChunk, lda, 0,
-              B + (tb ? (size_t)full * kChunk : (size_t)full * kChunk * ldb), ldb, 0, 0.0f,
-              part + (size_t)full * M * N, N, 0, 1, s);
-    return full + (rest > 0 ? 1 : 0);
+    sgemm(false, tb, M, N, kChunk, 1.0f, A, lda, kChunk, B, ldb, sb, 0.0f, part, N, (long long)M * N, nsplit, s,
+          false, last);
+    return nsplit;
 }
 
 template <int RPT>
