@@ -38,6 +38,7 @@ constexpr int NB = 128;                        // panel width
 constexpr int LW = 16;                         // leaf width
 constexpr int LT = 512;                        // leaf threads
 constexpr int kChunk = 512;                    // rows per split of a product over rows
+constexpr int kPanelTThreads = 1024;           // the panel T kernel's workgroup (its block merges are thread-parallel)
 constexpr float kTinySumsq = 8.271806e-25f;    // 2^-80
 
 // ---- wave reductions through DPP ----
@@ -364,18 +365,18 @@ __global__ __launch_bounds__(256) void qr_leaf_apply_kernel(float* __restrict__ 
 // Diagonal 16 x 16 blocks are the leaves' T; block column j above them is
 // T[0:16j, Bj] = -T[0:16j, 0:16j] (S[0:16j, Bj] T_jj), S = V^T V
 // (nbk x nbk, row-major).
-__global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict__ Ssum,
+__global__ __launch_bounds__(kPanelTThreads) void qr_panel_t_kernel(const float* __restrict__ Ssum,
                                                          const float* __restrict__ Tleaves, int nbk,
                                                          float* __restrict__ Tout) {
     __shared__ float S[NB][NB + 1];
     __shared__ float T[NB][NB + 1];
     __shared__ float X[NB][LW + 1];
     const int t = threadIdx.x;
-    for (int idx0 = 0; idx0 < NB * NB; idx0 += 256 * 8) {
-        float sv[8], tv[8];
+    for (int idx0 = 0; idx0 < NB * NB; idx0 += kPanelTThreads * 4) {
+        float sv[4], tv[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int idx = idx0 + u * 256 + t, i = idx >> 7, j = idx & (NB - 1);
+        for (int u = 0; u < 4; ++u) {
+            const int idx = idx0 + u * kPanelTThreads + t, i = idx >> 7, j = idx & (NB - 1);
             const bool in = i < nbk && j < nbk && j > i;
             const float sx = Ssum[in ? (size_t)i * nbk + j : 0];
             sv[u] = in ? sx : 0.0f;
@@ -386,8 +387,8 @@ __global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict
             tv[u] = din ? x : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int idx = idx0 + u * 256 + t;
+        for (int u = 0; u < 4; ++u) {
+            const int idx = idx0 + u * kPanelTThreads + t;
             S[idx >> 7][idx & (NB - 1)] = sv[u];
             T[idx >> 7][idx & (NB - 1)] = tv[u];
         }
@@ -397,7 +398,7 @@ __global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict
     for (int jb = 1; jb < nblk; ++jb) {
         const int j0 = jb * LW, rows = j0;   // block column jb, rows 0 .. j0 - 1
         // X = S[0:j0, Bj] T_jj
-        for (int idx = t; idx < rows * LW; idx += 256) {
+        for (int idx = t; idx < rows * LW; idx += kPanelTThreads) {
             const int r = idx / LW, c = idx % LW;
             float s = 0.0f;
 #pragma unroll
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict
         }
         __syncthreads();
         // T[0:j0, Bj] = -T[0:j0, 0:j0] X
-        for (int idx = t; idx < rows * LW; idx += 256) {
+        for (int idx = t; idx < rows * LW; idx += kPanelTThreads) {
             const int r = idx / LW, c = idx % LW;
             float s = 0.0f;
             for (int l = r; l < rows; ++l) s = fmaf(T[r][l], X[l][c], s);
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(256) void qr_panel_t_kernel(const float* __restrict
         }
         __syncthreads();
     }
-    for (int idx = t; idx < nbk * nbk; idx += 256) {
+    for (int idx = t; idx < nbk * nbk; idx += kPanelTThreads) {
         const int i = idx / nbk, j = idx - i * nbk;
         Tout[idx] = T[i][j];
     }
@@ -678,7 +679,7 @@ void qr_blocked_one(const float* a, float* q, float* r, int m, int n, int qc, in
             const int nsplit = gram(Vt, Vt, ldv, nbk, nbk, ldp, w.part, s);
             hipLaunchKernelGGL(sum_parts_kernel, dim3(grid_for((size_t)nbk * nbk)), dim3(256), 0, s, w.part, nsplit,
                                (size_t)nbk * nbk, w.W);
-            hipLaunchKernelGGL(qr_panel_t_kernel, dim3(1), dim3(256), 0, s, w.W, w.Tleaves, nbk, T);
+            hipLaunchKernelGGL(qr_panel_t_kernel, dim3(1), dim3(kPanelTThreads), 0, s, w.W, w.Tleaves, nbk, T);
         }
         // trailing matrix: A2 -= V (T^T (V^T A2))
         const int n2 = n - pe;
