@@ -4,7 +4,8 @@
 
 A step is one synchronous C-ABI call over one batch of synthetic input that
 is already resident in HBM (torch tensors on cuda:0, passed as device
-pointers).  W untimed steps, then K timed steps between two
+pointers; the output buffers allocated once before the steps, as a C caller
+holds them).  W untimed steps, then K timed steps between two
 synchronisations.  One JSON line on stdout: `value` = matrices/s over the
 timed steps; `roofline` = the dominant kernel's algorithmic bytes (or flops)
 per launch over its average duration, timed with HIP events on the
@@ -322,6 +323,93 @@ def workloads():
     return w
 
 
+class CAbi:
+    """The workloads' calls made as a C caller makes them: device pointers
+    straight into the C ABI, output buffers allocated once (`allocate`, before
+    any step) and written again by every call.  A step then holds the library
+    call alone; the inputs are resident and torch has nothing pending on its
+    stream, so no stream ordering is asked for (the Python API in
+    `metal_linalg_amd.api` adds its output allocations and, when torch's
+    stream has work pending, an event wait; `ms_per_step_python_api` times
+    it)."""
+
+    def __init__(self, lib):
+        self.lib, self.bufs, self.dry = lib, {}, False
+
+    def _out(self, key, specs):
+        if key not in self.bufs:
+            import torch
+
+            self.bufs[key] = [None if shape is None else
+                              torch.empty(shape, dtype=torch.float32 if dt == "f32" else torch.int32, device="cuda")
+                              for shape, dt in specs]
+        return self.bufs[key]
+
+    def _call(self, fn, *args):
+        if self.dry:
+            return
+        rc = fn(*[a.data_ptr() if hasattr(a, "data_ptr") else a for a in args])
+        if rc != self.lib.OK:
+            raise RuntimeError(self.lib.last_error().decode())
+
+    def allocate(self, wl, dev):
+        self.dry = True
+        try:
+            wl.call(self, dev)
+        finally:
+            self.dry = False
+
+    @staticmethod
+    def _dims(a):
+        b = 1
+        for d in a.shape[:-2]:
+            b *= int(d)
+        return tuple(a.shape[:-2]), b, int(a.shape[-2]), int(a.shape[-1])
+
+    def qr(self, a, mode="reduced"):
+        lead, b, m, n = self._dims(a)
+        k = min(m, n)
+        code = self.lib.QR_MODES[mode]
+        qc = 0 if code == 1 else (m if code == 2 else k)
+        rr = m if code == 2 else k
+        q, r = self._out(("qr", a.shape, mode), [(lead + (m, qc) if qc else None, "f32"), (lead + (rr, n), "f32")])
+        self._call(self.lib.qr_with_mode, a, b, m, n, code, q, r)
+
+    def eigh(self, a, lower=True, vectors=True):
+        lead, b, n, _ = self._dims(a)
+        w, v, info = self._out(("eigh", a.shape, vectors),
+                               [(lead + (n,), "f32"), (lead + (n, n) if vectors else None, "f32"), (lead, "u32")])
+        self._call(self.lib.eigh, a, b, n, int(bool(lower)), w, v, info)
+
+    def svd(self, a, vectors=True):
+        lead, b, m, n = self._dims(a)
+        k = min(m, n)
+        u, s, vt, info = self._out(("svd", a.shape, vectors),
+                                   [(lead + (m, k) if vectors else None, "f32"), (lead + (k,), "f32"),
+                                    (lead + (k, n) if vectors else None, "f32"), (lead, "u32")])
+        self._call(self.lib.svd, a, b, m, n, u, s, vt, info)
+
+    def cholesky(self, a, upper=False):
+        lead, b, n, _ = self._dims(a)
+        l, info = self._out(("cholesky", a.shape), [(lead + (n, n), "f32"), (lead, "u32")])
+        self._call(self.lib.cholesky, a, b, n, int(bool(upper)), l, info)
+
+    def lu_factor(self, a):
+        lead, b, n, _ = self._dims(a)
+        lu, piv, info = self._out(("lu", a.shape), [(lead + (n, n), "f32"), (lead + (n,), "u32"), (lead, "u32")])
+        self._call(self.lib.lu_factor, a, b, n, lu, piv, info)
+
+    def solve(self, a, rhs):
+        lead, b, n, _ = self._dims(a)
+        x, info = self._out(("solve", a.shape, rhs.shape), [(tuple(rhs.shape), "f32"), (lead, "u32")])
+        self._call(self.lib.solve, a, b, n, rhs, int(rhs.shape[-1]), x, info)
+
+    def solve_triangular(self, a, rhs, upper=False, unit=False):
+        lead, b, n, _ = self._dims(a)
+        (x,) = self._out(("trsm", a.shape, rhs.shape), [(tuple(rhs.shape), "f32")])
+        self._call(self.lib.solve_triangular, a, b, n, rhs, int(rhs.shape[-1]), int(bool(upper)), int(bool(unit)), x)
+
+
 def _arrays(x):
     if x is None:
         return []
@@ -466,15 +554,17 @@ def main():
     dev = {k: torch.from_numpy(np.ascontiguousarray(v)).to("cuda") for k, v in host.items()}
     torch.cuda.synchronize()
 
+    cabi = CAbi(_lib)
+    cabi.allocate(wl, dev)
     for _ in range(args.warmup):
-        wl.call(api, dev)
+        wl.call(cabi, dev)
     torch.cuda.synchronize()
 
     # the timed steps, with no events between the path's launches
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        wl.call(api, dev)
+        wl.call(cabi, dev)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
@@ -486,10 +576,19 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     for _ in range(args.steps):
-        wl.call(api, dev)
+        wl.call(cabi, dev)
     torch.cuda.synchronize()
     elapsed_events = time.perf_counter() - t1
     _lib.hip_set_timing(0)
+
+    # the same steps through the Python API (new output tensors per call)
+    wl.call(api, dev)
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.call(api, dev)
+    torch.cuda.synchronize()
+    elapsed_api = time.perf_counter() - t2
 
     # the path's kernels (one name, or several launched once per call each)
     names = wl.kernel if isinstance(wl.kernel, (list, tuple)) else [wl.kernel]
@@ -540,6 +639,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "ms_per_step_kernel_events": round(elapsed_events * 1e3 / args.steps, 5),
+        "ms_per_step_python_api": round(elapsed_api * 1e3 / args.steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -77,14 +77,17 @@ class _Arrays:
     def call(self, fn, *args):
         """fn(*args) under the library lock.  For tensors on the GPU the
         library's stream first waits for what torch has enqueued on its
-        current stream so far, this call's input conversions and output
-        allocations included: an event, not a host synchronisation.  The
-        library returns when its results are complete."""
+        current stream so far, this call's input conversions included: an
+        event, not a host synchronisation, and none at all when that stream
+        has nothing pending (the wait costs ~20 us per call).  The library
+        returns when its results are complete."""
         with _lib.lock:
             if self.torch and self.device.type == "cuda":
                 import torch
 
-                _check(_lib.hip_stream_wait(torch.cuda.current_stream(self.device).cuda_stream))
+                stream = torch.cuda.current_stream(self.device)
+                if not stream.query():
+                    _check(_lib.hip_stream_wait(stream.cuda_stream))
             _check(fn(*args))
 
     @staticmethod

@@ -234,14 +234,19 @@ __device__ __forceinline__ void trid_phases(float (&x)[kC * MC], MidLds& s, int 
     }
 }
 
-// Number of eigenvalues of the (split) tridiagonal below x: the LDL^T
-// recurrence of T - x I with tiny pivots replaced by -pivmin (slaebz's
-// count).  d and f = e^2 (shifted by one row) are read four rows at a time
-// from LDS; rows past n carry kPad and count nothing.
+// Number of eigenvalues of the (split) tridiagonal below x: the signs of
+// the LDL^T pivots t of T - x I (slaebz's count), each reciprocal 1/t
+// clamped to [-rbig, rbig], rbig = 1/pivmin: a pivot smaller than pivmin in
+// magnitude (zero included) acts as pivmin with its own sign, where slaebz
+// replaces it by -pivmin (one median instruction instead of a compare and a
+// select; either count is the exact one of a shift within a few pivmin of
+// x).  t stays finite (|f r| <= 2^126): no NaN, also across a split (f = 0).
+// d and f = e^2 (shifted by one row) are read four rows at a time from LDS;
+// rows past n carry kPad and count nothing.
 template <int N>
-__device__ __forceinline__ int sturm_count(const MidLds& s, float x, float pivmin) {
+__device__ __forceinline__ int sturm_count(const MidLds& s, float x, float rbig) {
     int cnt = 0;
-    float t = 1.0f;
+    float r = 1.0f;   // 1 / t of the row above (t = 1 before row 0)
 #pragma unroll
     for (int k0 = 0; k0 < N; k0 += 4) {
         const float4 dv = *reinterpret_cast<const float4*>(&s.d[k0]);
@@ -250,9 +255,9 @@ __device__ __forceinline__ int sturm_count(const MidLds& s, float x, float pivmi
         const float fk[4] = {fv.x, fv.y, fv.z, fv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            t = fmaf(-fk[j], __builtin_amdgcn_rcpf(t), dk[j] - x);
-            t = fabsf(t) < pivmin ? -pivmin : t;
+            const float t = fmaf(-fk[j], r, dk[j] - x);
             cnt += (int)(__float_as_uint(t) >> 31);
+            r = __builtin_amdgcn_fmed3f(__builtin_amdgcn_rcpf(t), -rbig, rbig);
         }
     }
     return cnt;
@@ -261,9 +266,9 @@ __device__ __forceinline__ int sturm_count(const MidLds& s, float x, float pivmi
 // The same count over the rows [lo_row, hi_row) of one block only (the
 // recurrence restarts at the block's first row by itself: e = 0 above it).
 template <int N>
-__device__ __forceinline__ int sturm_count_in(const MidLds& s, float x, float pivmin, int lo_row, int hi_row) {
+__device__ __forceinline__ int sturm_count_in(const MidLds& s, float x, float rbig, int lo_row, int hi_row) {
     int cnt = 0;
-    float t = 1.0f;
+    float r = 1.0f;
     const unsigned span = (unsigned)(hi_row - lo_row);
 #pragma unroll
     for (int k0 = 0; k0 < N; k0 += 4) {
@@ -273,8 +278,8 @@ __device__ __forceinline__ int sturm_count_in(const MidLds& s, float x, float pi
         const float fk[4] = {fv.x, fv.y, fv.z, fv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            t = fmaf(-fk[j], __builtin_amdgcn_rcpf(t), dk[j] - x);
-            t = fabsf(t) < pivmin ? -pivmin : t;
+            const float t = fmaf(-fk[j], r, dk[j] - x);
+            r = __builtin_amdgcn_fmed3f(__builtin_amdgcn_rcpf(t), -rbig, rbig);
             const int neg = (int)(__float_as_uint(t) >> 31);
             cnt += (unsigned)(k0 + j - lo_row) < span ? neg : 0;
         }
@@ -442,6 +447,7 @@ __global__ __launch_bounds__(kThreads) void eigh_mid_values_kernel(const float* 
     const float pivmin = kSafeMin * fmaxf(1.0f, e2max);
     const float slack = 2.1f * 2.0f * kEps * tnorm * (float)n + 4.2f * pivmin;
     const float atol = fmaxf(kEps * tnorm, 2.0f * pivmin);
+    const float rbig = 1.0f / pivmin;
 
     // 4. bisection: thread c brackets the (c - bs)-th smallest eigenvalue
     // of its block
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void eigh_mid_values_kernel(const float* 
         // equal divisions of the Gershgorin interval, and every thread takes
         // its bracket from those counts
         const float gh = (g1 - g0) / (float)(N + 1);
-        if (c < N) s.cnt[c] = sturm_count<N>(s, fmaf((float)(c + 1), gh, g0), pivmin);
+        if (c < N) s.cnt[c] = sturm_count<N>(s, fmaf((float)(c + 1), gh, g0), rbig);
         __syncthreads();
 #pragma unroll 4
         for (int i = 0; i < N; ++i) {
@@ -470,7 +476,7 @@ __global__ __launch_bounds__(kThreads) void eigh_mid_values_kernel(const float* 
         steps = 1;
         while (steps < kMaxBisect) {
             const float mid = 0.5f * (lo + hi);
-            const int cm = sturm_count<N>(s, mid, pivmin);
+            const int cm = sturm_count<N>(s, mid, rbig);
             if (cm > c) hi = mid;
             else lo = mid;
             ++steps;
@@ -494,7 +500,7 @@ __global__ __launch_bounds__(kThreads) void eigh_mid_values_kernel(const float* 
                 const bool done = !mine || single || hi - lo <= fmaxf(atol, 2.0f * kEps * fmaxf(fabsf(lo), fabsf(hi)));
                 if (!__syncthreads_or(!done)) break;
                 const float mid = 0.5f * (lo + hi);
-                const int cm = sturm_count_in<N>(s, mid, pivmin, bs, be);
+                const int cm = sturm_count_in<N>(s, mid, rbig, bs, be);
                 if (cm > j) hi = mid;
                 else lo = mid;
                 ++steps;

@@ -169,14 +169,20 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
     }
 }
 
-// Number of eigenvalues of the (split) tridiagonal below x: the LDL^T
-// recurrence of T - x I with tiny pivots replaced by -pivmin (LAPACK
-// slaebz's count).  d and f = e^2 (shifted by one row) are read four rows at
-// a time from LDS; rows past n carry kPad and count nothing.
+// Number of eigenvalues of the (split) tridiagonal below x: the signs of
+// the LDL^T pivots t of T - x I (LAPACK slaebz's count), where each
+// reciprocal 1/t is clamped to [-rbig, rbig], rbig = 1/pivmin: a pivot
+// smaller than pivmin in magnitude (zero included) acts as pivmin with its
+// own sign, where slaebz replaces it by -pivmin (one median instruction here
+// instead of a compare and a select; either count is the exact one of a
+// shift within a few pivmin of x).  t stays finite (|f r| <= 2^126), so no
+// NaN can arise, also across a split (f = 0).  d and f = e^2 (shifted by one
+// row) are read four rows at a time from LDS; rows past n carry kPad and
+// count nothing.
 template <int N>
-__device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float pivmin) {
+__device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float rbig) {
     int cnt = 0;
-    float t = 1.0f;
+    float r = 1.0f;   // 1 / t of the row above (t = 1 before row 0)
 #pragma unroll
     for (int k0 = 0; k0 < N; k0 += 4) {
         const float4 dv = *reinterpret_cast<const float4*>(&s.d[k0]);
@@ -185,9 +191,9 @@ __device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float p
         const float fk[4] = {fv.x, fv.y, fv.z, fv.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            t = fmaf(-fk[j], __builtin_amdgcn_rcpf(t), dk[j] - x);
-            t = fabsf(t) < pivmin ? -pivmin : t;
+            const float t = fmaf(-fk[j], r, dk[j] - x);
             cnt += (int)(__float_as_uint(t) >> 31);
+            r = __builtin_amdgcn_fmed3f(__builtin_amdgcn_rcpf(t), -rbig, rbig);
         }
     }
     return cnt;
@@ -513,6 +519,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 
     const float pivmin = kSafeMin * fmaxf(1.0f, e2max);
     const float slack = 2.1f * 2.0f * kEps * tnorm * (float)nn + 4.2f * pivmin;
     const float atol = fmaxf(kEps * tnorm, 2.0f * pivmin);
+    const float rbig = 1.0f / pivmin;
 
     // A diagonal T (every coupling split, e.g. A = a multiple of I, or the
     // zero matrix of a non-finite input): its eigenpairs are (d_j, e_j)
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 
     float lo = g0, hi = g1;
     int steps = 0;
     if (!all_diag) {
-        s.cnt[c] = sturm_count<N>(s, fmaf((float)(c + 1), gh, g0), pivmin);
+        s.cnt[c] = sturm_count<N>(s, fmaf((float)(c + 1), gh, g0), rbig);
         wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < N; ++i) {
@@ -560,7 +567,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 
     }
     while (!all_diag && steps < kMaxBisect) {
         const float mid = 0.5f * (lo + hi);
-        const int cm = sturm_count<N>(s, mid, pivmin);
+        const int cm = sturm_count<N>(s, mid, rbig);
         if (cm > c) {
             hi = mid;
         } else {
