@@ -161,6 +161,9 @@ __device__ __forceinline__ float group_lane(float v, int j, int lane) {
     if constexpr (G == 64) {
         return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
     } else if constexpr (G == 32) {
+        // five VALU instructions (the SGPR results go back to VGPRs for the
+        // half-select), but off LDS: an LDS permute here put its round trip
+        // on every step's critical path (config 1: 71.5 -> 73.9 us)
         const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
         const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j + 32));
         return lane >= 32 ? hi : lo;
@@ -294,31 +297,36 @@ __global__ __launch_bounds__(64) void qr_fixed_kernel(const float* __restrict__ 
     amax = group_max<G>(amax);
     bad = group_or<G>(bad);
     const int e = bad ? 0 : scale_exponent(amax);
+    // a matrix with a NaN or an infinity is factored as it is (the non-finite
+    // values stay inside its lane group: every exchange, LDS rows, readlanes
+    // and shuffles, is within the group) and written as NaN below
 #pragma unroll
-    for (int r = 0; r < M; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -e);
+    for (int r = 0; r < M; ++r) x[r] = ldexpf(x[r], -e);
 
     float myscale = 1.0f;
     qr_fixed_step<0, M, N, G, LD>(x, vsh[g], tsh[g], c, lane, myscale);
-    // lane c's reflector below the diagonal, scaled now
-#pragma unroll
-    for (int r = 0; r < M; ++r) x[r] = r > c ? x[r] * myscale : x[r];
 
     if (live && c < N) {
         float* out_r = Rout + mat * N * N;
-        const float unscale = ldexpf(1.0f, e);
+        const float unscale = bad ? qnan() : ldexpf(1.0f, e);   // 0 * NaN: the zeros below too
 #pragma unroll
-        for (int r = 0; r < N; ++r) out_r[(size_t)r * N + c] = bad ? qnan() : (c >= r ? x[r] * unscale : 0.0f);
+        for (int r = 0; r < N; ++r) out_r[(size_t)r * N + c] = (c >= r ? x[r] : 0.0f) * unscale;
     }
     if (qc == 0) return;
-    // lane c's column becomes its reflector: 1 at row c, zero above (the
-    // columns of a square Q past K do not exist here: M >= N = K)
+    // lane c's column becomes its reflector, scaled now: 1 at row c, zero
+    // above (the columns of a square Q past K do not exist here: M >= N = K)
 #pragma unroll
-    for (int r = 0; r < M; ++r) x[r] = r < c ? 0.0f : (r == c ? 1.0f : x[r]);
+    for (int r = 0; r < M; ++r) x[r] = r < c ? 0.0f : (r == c ? 1.0f : x[r] * myscale);
     qr_fixed_qstep<N - 1, M, N, LD>(x, vsh[g], tsh[g], c, (int)qc);
     if (live && c < N) {
         float* out_q = Q + mat * M * N;
+        if (__ballot(bad) == 0) {   // uniform: no select per entry
 #pragma unroll
-        for (int r = 0; r < M; ++r) out_q[(size_t)r * N + c] = bad ? qnan() : x[r];
+            for (int r = 0; r < M; ++r) out_q[(size_t)r * N + c] = x[r];
+        } else {
+#pragma unroll
+            for (int r = 0; r < M; ++r) out_q[(size_t)r * N + c] = bad ? qnan() : x[r];
+        }
     }
 }
 
