@@ -51,6 +51,13 @@ constexpr float kPad = 0x1p100f;             // the diagonal of padding rows: ne
 constexpr float kOrtol = 1e-3f;               // close eigenvalues: gap <= kOrtol |T| (sstein's ORTOL)
 constexpr int kMaxBisect = 64;
 constexpr int kBT = 8;                       // reflectors staged per back-transform block
+#ifndef EIGH_DOT_D
+#define EIGH_DOT_D 4
+#endif
+#ifndef EIGH_R2_D
+#define EIGH_R2_D 2
+#endif
+
 // n = 64 with vectors runs in two launches (the first fits four waves per
 // SIMD, the vectors need more VGPRs): per matrix the first leaves d, e, 1/e,
 // tau, the eigenvalue and the diagonal-path row of each lane, and three
@@ -88,6 +95,79 @@ __device__ __forceinline__ float dot_tail(const float* x, const float* y) {
     return (s0 + s1) + (s2 + s3);
 }
 
+// Rows A0 .. N-1 (A0 a multiple of 4) of an LDS vector as float4 chunks,
+// each read D chunks before its use: the reads of later chunks are in
+// flight while the current one is consumed, instead of a full LDS round
+// trip every few rows.  The schedule barrier after each chunk keeps the
+// compiler from hoisting every read to the top (which would hold the whole
+// vector in VGPRs beside the column).
+template <int A0, int N>
+__device__ __forceinline__ float4 lds_chunk(const float* a, int q) {
+    return *reinterpret_cast<const float4*>(a + A0 + 4 * q);
+}
+
+// sum of v[r] x[r] over rows A0 .. N-1 into four partial sums by r mod 4
+template <int A0, int N, int D>
+__device__ __forceinline__ float lds_dot(const float* v, const float (&x)[N]) {
+    constexpr int NC = (N - A0) / 4;
+    float4 b[NC];
+    float dp0 = 0.0f, dp1 = 0.0f, dp2 = 0.0f, dp3 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < (D < NC ? D : NC); ++q) b[q] = lds_chunk<A0, N>(v, q);
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+        if (q + D < NC) b[q + D] = lds_chunk<A0, N>(v, q + D);
+        const int r = A0 + 4 * q;
+        dp0 = fmaf(b[q].x, x[r], dp0);
+        dp1 = fmaf(b[q].y, x[r + 1], dp1);
+        dp2 = fmaf(b[q].z, x[r + 2], dp2);
+        dp3 = fmaf(b[q].w, x[r + 3], dp3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return (dp0 + dp1) + (dp2 + dp3);
+}
+
+// x[r] -= v[r] w + b[r] u over rows A0 .. N-1
+template <int A0, int N, int D>
+__device__ __forceinline__ void lds_rank2(float (&x)[N], const float* v, const float* bw, float w, float u) {
+    constexpr int NC = (N - A0) / 4;
+    float4 p[NC], q4[NC];
+#pragma unroll
+    for (int q = 0; q < (D < NC ? D : NC); ++q) {
+        p[q] = lds_chunk<A0, N>(v, q);
+        q4[q] = lds_chunk<A0, N>(bw, q);
+    }
+#pragma unroll
+    for (int q = 0; q < NC; ++q) {
+        if (q + D < NC) {
+            p[q + D] = lds_chunk<A0, N>(v, q + D);
+            q4[q + D] = lds_chunk<A0, N>(bw, q + D);
+        }
+        const int r = A0 + 4 * q;
+        x[r] = fmaf(-p[q].x, w, fmaf(-q4[q].x, u, x[r]));
+        x[r + 1] = fmaf(-p[q].y, w, fmaf(-q4[q].y, u, x[r + 1]));
+        x[r + 2] = fmaf(-p[q].z, w, fmaf(-q4[q].z, u, x[r + 2]));
+        x[r + 3] = fmaf(-p[q].w, w, fmaf(-q4[q].w, u, x[r + 3]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Global memory as the compiler's address space 1: stores through such a
+// pointer are global_store (a generic pointer gives flat_store, which also
+// counts against the LDS wait counter).
+typedef __attribute__((address_space(1))) float gfloat;
+
+// A pointer that is the same on every lane, moved to SGPRs (otherwise a
+// 64-bit VGPR pair that the register allocator spills and reloads), as a
+// global pointer.
+__device__ __forceinline__ gfloat* uniform_gptr(float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (gfloat*)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ gfloat* global_ptr(float* p) { return (gfloat*)reinterpret_cast<uint64_t>(p); }
+
 // Where v_K's entries K+1 .. n-1 start in the packed reflector storage:
 // after v_0 .. v_{K-1} (n-1, n-2, ... entries).  The whole set, n(n-1)/2 - 1
 // floats, fits in V's n x n.
@@ -109,7 +189,7 @@ __device__ __forceinline__ float group_bcast(float v, int src) {
 // back-transformation), and read back as a broadcast for the products.
 // Then the symmetric rank-2 update of the trailing block, w through bc.
 template <int K, int N>
-__device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c, int n, float* vg) {
+__device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c, int n, gfloat* vg) {
     if constexpr (K + 2 < N) {
         if (K + 2 < n) {
             // c laundered: otherwise the compiler precomputes the lane masks
@@ -136,34 +216,25 @@ __device__ __forceinline__ void tridiag_step(float (&x)[N], EighLds<N>& s, int c
                 s.e[K] = beta;
                 s.tau[K] = tau;
             }
+            // v^T x_c from the aligned row at or before K+1: v is zero in
+            // the rows up to K (every lane wrote its entry, zero at and left
+            // of K), so those rows add exact zeros
+            constexpr int A0 = (K + 1) / 4 * 4;
             wave_lds_sync();
-            // v^T x_c, v read from LDS 16 rows at a time (the schedule
-            // barriers keep the compiler from holding all of v in VGPRs
-            // beside the column)
-            float dp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            {
-                const float* vr = s.vr[K & 1];
-#pragma unroll
-                for (int r = K + 1; r < N; ++r) {
-                    dp[r & 3] = fmaf(vr[r], x[r], dp[r & 3]);
-                    if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            const float p = act ? tau * ((dp[0] + dp[1]) + (dp[2] + dp[3])) : 0.0f;
+            float dv = lds_dot<A0, N, EIGH_DOT_D>(s.vr[K & 1], x);
+            __asm__ volatile("" : "+v"(dv));   // computed by every lane: no branch around the reads
+            const float p = act ? tau * dv : 0.0f;
             const float half = 0.5f * tau * group_sum_dpp<N>(p * vc);
             const float w = fmaf(-half, vc, p);
             float* bc = s.bc[K & 1];
             bc[c] = w;
             wave_lds_sync();
-            {
-                // every lane: outside the trailing block vc = w = 0, so the
-                // update leaves x as it is (no divergent branch, whose merge
-                // would copy the column).  v is read again from LDS: holding
-                // it across the barrier would keep N more VGPRs live.
-                const float* vr = s.vr[K & 1];
-#pragma unroll
-                for (int r = K + 1; r < N; ++r) x[r] = fmaf(-vr[r], w, fmaf(-bc[r], vc, x[r]));
-            }
+            // every lane: outside the trailing block vc = w = 0, so the
+            // update leaves x as it is (no divergent branch, whose merge
+            // would copy the column); v and w are zero in the rows up to K,
+            // which are left as they are.  v is read again from LDS: holding
+            // it across the barrier would keep N more VGPRs live.
+            lds_rank2<A0, N, EIGH_R2_D>(x, s.vr[K & 1], bc, w, vc);
         }
         tridiag_step<K + 1, N>(x, s, c, n, vg);
     }
@@ -197,6 +268,57 @@ __device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float r
         }
     }
     return cnt;
+}
+
+// Column c of the symmetric matrix whose LOWER (or upper) triangle is read,
+// for lane c of its N-lane group.  Every row is read whole across the lanes
+// (lane c: entry (r, c), coalesced); the entries outside the read triangle
+// are then replaced by their mirror images, which other lanes hold: lanes
+// stage their columns in LDS, CH at a time, and lane c takes entry c of
+// column r from there.  The values read outside the triangle are never used
+// (a NaN there changes nothing).  Reads stay inside the n x n matrix; rows
+// and columns past n are zero.
+template <int N, bool LOWER>
+__device__ __forceinline__ void load_symmetric(float (&x)[N], EighLds<N>& s, const float* src, int c, int nn) {
+    if (nn == N) {   // the whole group's shape: row offsets are constants
+        const float* col = src + c;
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            x[r] = col[r * N];
+            // 16 loads at a time: their addresses are not all held at once
+            if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+        }
+    } else {
+        const int cc = c < nn ? c : nn - 1;
+#pragma unroll
+        for (int r = 0; r < N; ++r) {
+            const int rr = r < nn ? r : nn - 1;
+            x[r] = src[rr * nn + cc];   // 32-bit offsets: n <= 64
+            if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int r = 0; r < N; ++r) x[r] = (r < nn && c < nn) ? x[r] : 0.0f;
+    }
+    constexpr int CH = N < 16 ? N : 16;
+    constexpr int LD = N + 4;
+    float* stg = &s.bt[0][0][0];   // CH x LD floats, free until the back-transform
+    static_assert(CH * LD <= 2 * kBT * (N + 4), "mirror staging fits the back-transform block");
+#pragma unroll
+    for (int j = 0; j < N / CH; ++j) {
+        if (c >= j * CH && c < (j + 1) * CH) {   // stores only
+#pragma unroll
+            for (int r = 0; r < N; r += 4)
+                *reinterpret_cast<float4*>(&stg[(c - j * CH) * LD + r]) = make_float4(x[r], x[r + 1], x[r + 2], x[r + 3]);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int r = j * CH; r < (j + 1) * CH; ++r) {
+            const bool take = LOWER ? r >= c : r <= c;
+            const float m = stg[(r - j * CH) * LD + c];
+            x[r] = take ? x[r] : m;
+        }
+        wave_lds_sync();
+    }
 }
 
 // x <- x / |x|_2, scaled by its largest entry first.
@@ -426,35 +548,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 
     const int nn = (int)n;
     const size_t per = (size_t)n * n;
 
-    // 1. the read triangle, mirrored into a full symmetric matrix: entry r
-    // of lane c's column comes from the column (coalesced across lanes) in
-    // the read triangle and from row c (served from L2) outside it, one
-    // load per entry.  Every load is unconditional (clamped into the
-    // matrix) so that they are all in flight together.
+    // 1. the read triangle, mirrored into a full symmetric matrix
     float x[N];
     float amax = 0.0f;
     int bad = 0;
     {
-        const int cc = c < nn ? c : nn - 1;
         const float* src = A + (live ? mat : 0) * per;
+        if (lower) load_symmetric<N, true>(x, s, src, c, nn);
+        else load_symmetric<N, false>(x, s, src, c, nn);
+        // every entry now comes from the read triangle (or is a zero pad):
+        // the largest magnitude, and a NaN or infinity anywhere (v * 0 is
+        // NaN exactly for those)
+        float nz = 0.0f;
 #pragma unroll
         for (int r = 0; r < N; ++r) {
-            const int rr = r < nn ? r : nn - 1;
-            const bool take = lower ? r >= c : r <= c;
-            const int off = take ? rr * nn + cc : cc * nn + rr;   // 32-bit: n <= 64
-            x[r] = src[off];
-            // 16 loads at a time: their addresses are not all held at once
-            if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+            amax = fmaxf(amax, fabsf(x[r]));
+            nz = fmaf(x[r], 0.0f, nz);
         }
-#pragma unroll
-        for (int r = 0; r < N; ++r) {
-            const bool in = live && r < nn && c < nn;
-            const bool take = lower ? r >= c : r <= c;
-            const float v = in ? x[r] : 0.0f;
-            amax = fmaxf(amax, fabsf(v));
-            bad |= in && take && !finite_f(v);
-            x[r] = v;
-        }
+        bad = (live && nz != 0.0f) ? 1 : 0;   // nz is 0 or NaN
     }
     amax = group_max<N>(amax);
     bad = group_or<N>(bad);
@@ -463,7 +574,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(SPLIT ? 4 : 
     for (int r = 0; r < N; ++r) x[r] = bad ? 0.0f : ldexpf(x[r], -ex);
 
     // 2. tridiagonalise: d, e, tau; v_k goes to V's storage (packed)
-    float* vg = (VEC && live) ? V + mat * per : nullptr;
+    // one matrix per wave: the base in SGPRs
+    gfloat* vg = MPW == 1 ? uniform_gptr((VEC && live) ? V + mat * per : nullptr)
+                          : global_ptr((VEC && live) ? V + mat * per : nullptr);
     tridiag_step<0, N>(x, s, c, nn, vg);
     {
         float diag = 0.0f, sub = 0.0f;
