@@ -392,12 +392,23 @@ __global__ __launch_bounds__(64) void svd_bdsqr_kernel(float* __restrict__ ws, f
             const float gq = sqrtf(fmaf(f, f, 1.0f));
             f = ((x0 - z0) * (x0 + z0) + h0 * ((y0 / (f + copysignf(gq, f))) - h0)) / x0;
             float c = 1.0f, sn = 1.0f, x = x0;
+            // e[j+1] and q[j+1] are read one rotation ahead: step j writes
+            // only e[j] and q[j], so step j+1's entries are final when step
+            // j starts, and their LDS latency hides behind step j's chain
+            float gn = s.e[l + 1], yn = s.q[l + 1];
 #pragma unroll
             for (int j = 0; j < NN - 1; ++j) {
-                if (j >= l && j < k) {
+                // l and k laundered per step: two scalar compares here,
+                // instead of the 63 compares precomputed at the sweep's start
+                // and spilled to VGPR lanes
+                int lj = l, kj = k;
+                asm volatile("" : "+s"(lj), "+s"(kj));
+                if (j >= lj && j < kj) {
                     const int i = j + 1;
-                    float g = s.e[i];
-                    float y = s.q[i];
+                    float g = gn;
+                    float y = yn;
+                    gn = s.e[j + 2 <= NN ? j + 2 : NN];
+                    yn = s.q[j + 2 <= NN ? j + 2 : NN];
                     float h = sn * g;
                     g = c * g;
                     float cz, sz;
