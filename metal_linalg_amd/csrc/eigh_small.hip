@@ -345,16 +345,20 @@ __device__ __forceinline__ void normalize(float (&x)[N]) {
 // refl_offset(K, n)) in blocks of kBT: a block is loaded (element c of each
 // reflector by lane c) one block ahead, stored to LDS and read as
 // broadcasts.  Reflectors past n - 3 are clamped into range and never used.
+// The loads are masked (zero at and above row k) only when the block is
+// staged, a block later: a select right after them would wait for them.
+__device__ __forceinline__ int bt_k(int kb, int i, int n) {
+    const int kmax = n - 3 > 0 ? n - 3 : 0;
+    return kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
+}
 template <int N>
 __device__ __forceinline__ void bt_fetch(float (&nx)[kBT], const float* vg, int kb, int c, int n) {
-    const int kmax = n - 3 > 0 ? n - 3 : 0;
 #pragma unroll
     for (int i = 0; i < kBT; ++i) {
-        const int k = kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
+        const int k = bt_k(kb, i, n);
         const bool in = c > k && c < n;   // v_k is zero at and above row k
         const int off = refl_offset(k, n);
-        const float v = vg[in ? off + c - k - 1 : off];
-        nx[i] = in ? v : 0.0f;
+        nx[i] = vg[in ? off + c - k - 1 : off];
     }
 }
 
@@ -366,7 +370,10 @@ __device__ __forceinline__ void backtransform_step(float (&x)[N], EighLds<N>& s,
         constexpr int I = ((N - 3) - K) % kBT;   // position in the block
         if constexpr (I == 0) {
 #pragma unroll
-            for (int i = 0; i < kBT; ++i) s.bt[B & 1][i][c] = nx[i];
+            for (int i = 0; i < kBT; ++i) {
+                const int k = bt_k(K, i, n);
+                s.bt[B & 1][i][c] = (c > k && c < n) ? nx[i] : 0.0f;
+            }
             if constexpr (K - kBT >= 0) bt_fetch<N>(nx, vg, K - kBT, c, n);
             wave_lds_sync();
         }
