@@ -281,16 +281,20 @@ struct PinnedSlots {
     }
 };
 
+// Device slots of the all-pinned path: every chunk is queued at once, and
+// chunk k reuses slot k mod kSlots after chunk k - kSlots's download.
+constexpr int kSlots = 4;
+
 struct Staging {
     PinnedSlots pinned;
     hipStream_t copy = nullptr, down = nullptr;   // host-to-device, device-to-host (the link is full duplex)
-    hipEvent_t ev_in[2] = {}, ev_kern[2] = {}, ev_out[2] = {};
+    hipEvent_t ev_in[kSlots] = {}, ev_kern[kSlots] = {}, ev_out[kSlots] = {};
     bool ready = false;
     void init() {
         if (ready) return;
         MLA_HIP(hipStreamCreate(&copy));   // default priority
         MLA_HIP(hipStreamCreate(&down));
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kSlots; ++i) {
             MLA_HIP(hipEventCreateWithFlags(&ev_in[i], hipEventDisableTiming));
             MLA_HIP(hipEventCreateWithFlags(&ev_kern[i], hipEventDisableTiming));
             MLA_HIP(hipEventCreateWithFlags(&ev_out[i], hipEventDisableTiming));
@@ -432,6 +436,13 @@ void Call::batched(uint32_t batch, const std::vector<Slice>& slices, const Chunk
     Staging& st = staging();
     st.init();
     const size_t slot_bytes = in_bytes + out_bytes;
+    bool all_pinned = true;
+    for (size_t i = 0; i < ns; ++i)
+        if (staged[i] && !pinned[i]) all_pinned = false;
+    if (all_pinned) {
+        pinned_chunks(batch, chunk, slices, staged, off, in_bytes, slot_bytes, launch);
+        return;
+    }
     char* dslot[2] = {static_cast<char*>(take(slot_bytes)), static_cast<char*>(take(slot_bytes))};
     char* hslot[2] = {static_cast<char*>(st.pinned.get(0, slot_bytes)), static_cast<char*>(st.pinned.get(1, slot_bytes))};
     const uint32_t nchunks = (uint32_t)((batch + chunk - 1) / chunk);
@@ -494,6 +505,51 @@ void Call::batched(uint32_t batch, const std::vector<Slice>& slices, const Chunk
         if (k > 0) drain(k - 1);
     }
     drain(nchunks - 1);
+}
+
+// Every host buffer is the caller's pinned memory: no host copies, so the
+// host only queues.  Uploads run back to back on the copy stream, each
+// chunk's kernel waits for its upload, its download for its kernel, and an
+// upload into a reused slot for that slot's previous download; the host
+// waits once, for the last download.
+void Call::pinned_chunks(uint32_t batch, uint32_t chunk, const std::vector<Slice>& slices,
+                         const std::vector<char>& staged, const std::vector<size_t>& off, size_t in_bytes,
+                         size_t slot_bytes, const ChunkLaunch& launch) {
+    Staging& st = staging();
+    const size_t ns = slices.size();
+    const uint32_t nchunks = (uint32_t)((batch + chunk - 1) / chunk);
+    const int nslots = (int)std::min<uint32_t>(kSlots, nchunks);
+    char* dslot[kSlots] = {};
+    for (int s = 0; s < nslots; ++s) dslot[s] = static_cast<char*>(take(slot_bytes));
+    std::vector<void*> dev(ns);
+    for (uint32_t k = 0; k < nchunks; ++k) {
+        const int s = (int)(k % kSlots);
+        const uint32_t b0 = k * chunk, nb = std::min(chunk, batch - b0);
+        if (k >= (uint32_t)kSlots) MLA_HIP(hipStreamWaitEvent(st.copy, st.ev_out[s], 0));
+        for (size_t i = 0; i < ns; ++i)
+            if (staged[i] == 1)
+                MLA_HIP(hipMemcpyAsync(dslot[s] + off[i], static_cast<const char*>(slices[i].in) + (size_t)b0 * slices[i].per,
+                                       (size_t)nb * slices[i].per, hipMemcpyHostToDevice, st.copy));
+        MLA_HIP(hipEventRecord(st.ev_in[s], st.copy));
+        MLA_HIP(hipStreamWaitEvent(dev_.stream, st.ev_in[s], 0));
+        for (size_t i = 0; i < ns; ++i) {
+            const auto& sl = slices[i];
+            if (staged[i] == 1) dev[i] = dslot[s] + off[i];
+            else if (staged[i] == 2) dev[i] = dslot[s] + in_bytes + off[i];
+            else if (sl.in) dev[i] = const_cast<char*>(static_cast<const char*>(sl.in)) + (size_t)b0 * sl.per;
+            else dev[i] = sl.out ? static_cast<char*>(sl.out) + (size_t)b0 * sl.per : nullptr;
+        }
+        launch(dev.data(), nb, dev_.stream);
+        MLA_HIP(hipEventRecord(st.ev_kern[s], dev_.stream));
+        MLA_HIP(hipStreamWaitEvent(st.down, st.ev_kern[s], 0));
+        for (size_t i = 0; i < ns; ++i)
+            if (staged[i] == 2)
+                MLA_HIP(hipMemcpyAsync(static_cast<char*>(slices[i].out) + (size_t)b0 * slices[i].per,
+                                       dslot[s] + in_bytes + off[i], (size_t)nb * slices[i].per, hipMemcpyDeviceToHost,
+                                       st.down));
+        MLA_HIP(hipEventRecord(st.ev_out[s], st.down));
+    }
+    MLA_HIP(hipEventSynchronize(st.ev_out[(nchunks - 1) % kSlots]));
 }
 
 void Call::finish() {

@@ -86,11 +86,12 @@ public:
     uint32_t chunk_size(uint32_t batch, const std::vector<Slice>& slices) const;
     // Runs a batched call.  Device buffers are used in place and the whole
     // batch is one launch.  When any buffer is host memory the batch runs in
-    // chunks through pinned staging buffers, two chunks in flight: the host
-    // copies of one chunk, the transfers of another and the kernels of a
-    // third overlap (uploads and downloads on two more streams, ordered by
-    // events).  Every
-    // host output is written when this returns; finish() still follows.
+    // chunks (uploads and downloads on two more streams, ordered by events).
+    // Pageable buffers go through pinned staging, two chunks in flight: the
+    // host copies of one chunk, the transfers of another and the kernels of
+    // a third overlap.  When every host buffer is the caller's pinned memory
+    // the chunks are all queued at once over four device slots.  Every host
+    // output is written when this returns; finish() still follows.
     void batched(uint32_t batch, const std::vector<Slice>& slices, const ChunkLaunch& launch);
 
 private:
@@ -100,6 +101,9 @@ private:
     struct Back { void* host; void* dev; size_t bytes; };
     std::vector<Back> back_;
     void* take(size_t bytes);
+    void pinned_chunks(uint32_t batch, uint32_t chunk, const std::vector<Slice>& slices,
+                       const std::vector<char>& staged, const std::vector<size_t>& off, size_t in_bytes,
+                       size_t slot_bytes, const ChunkLaunch& launch);
 };
 
 // Kernel timing for measurement (bench.py): when enabled, launch sites
