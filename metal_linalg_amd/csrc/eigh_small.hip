@@ -281,10 +281,18 @@ __device__ __forceinline__ int sturm_count(const EighLds<N>& s, float x, float r
 template <int N, bool LOWER>
 __device__ __forceinline__ void load_symmetric(float (&x)[N], EighLds<N>& s, const float* src, int c, int nn) {
     if (nn == N) {   // the whole group's shape: row offsets are constants
-        const float* col = src + c;
+        // a lane outside the read triangle reads row r's diagonal entry in
+        // place of its own (the value is replaced below): only the read
+        // triangle's cache lines are fetched
+        // a buffer resource over the group's matrix: SGPR base, 32-bit
+        // byte offsets per lane, the row's offset an immediate
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, N * N * 4, 0x00020000);
+        const int cb = 4 * c;
 #pragma unroll
         for (int r = 0; r < N; ++r) {
-            x[r] = col[r * N];
+            const int vo = 4 * N * r + (LOWER ? min(cb, 4 * r) : max(cb, 4 * r));
+            x[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, 0, 0));
             // 16 loads at a time: their addresses are not all held at once
             if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
         }
