@@ -453,10 +453,19 @@ __global__ __launch_bounds__(256) void lu_mid_kernel(const float* A, float* __re
         if (piv == 0.0f && info == 0) info = k + 1;
         __syncthreads();
         if (t == 0) a[k * ld + k] = piv;
-        // rows to the four waves in turn, columns to the lanes
-        for (int r = k + 1 + wv; r < nn; r += 4) {
-            const float lr = a[r * ld + k];
-            for (int c = k + 1 + lane; c < nn; c += 64) a[r * ld + c] = fmaf(-lr, a[k * ld + c], a[r * ld + c]);
+        // rows to the four waves in turn, columns to the lanes: a lane's (at
+        // most two) columns are the same for every row, so their pivot-row
+        // entries are read once, into registers
+        {
+            const int c0 = k + 1 + lane, c1 = c0 + 64;
+            const bool in0 = c0 < nn, in1 = c1 < nn;
+            const float u0 = in0 ? a[k * ld + c0] : 0.0f;
+            const float u1 = in1 ? a[k * ld + c1] : 0.0f;
+            for (int r = k + 1 + wv; r < nn; r += 4) {
+                const float lr = a[r * ld + k];
+                if (in0) a[r * ld + c0] = fmaf(-lr, u0, a[r * ld + c0]);
+                if (in1) a[r * ld + c1] = fmaf(-lr, u1, a[r * ld + c1]);
+            }
         }
         __syncthreads();
     }
