@@ -89,3 +89,19 @@ def test_pinned_host_buffers(cuda, api):
     xp, _ = api.solve(cuda.from_numpy(g).pin_memory(), cuda.from_numpy(b))   # b pinned by the call
     xd, _ = api.solve(dev(cuda, g), dev(cuda, b))
     assert same(xp, xd)
+
+
+def test_pinned_host_buffers_many_chunks(cuda, api):
+    """Every host buffer pinned: all chunks are queued at once over four
+    device slots, each reused once its previous chunk's download is done.
+    Ten chunks (QR, ~2730 matrices each) and six (eigh, 1024 each), the last
+    partial: same bits as the device call."""
+    a = config1_qr(batch=25001, seed=38)
+    qp, rp = api.qr(cuda.from_numpy(a).pin_memory())
+    assert qp.is_pinned() and rp.is_pinned()
+    qd, rd = api.qr(dev(cuda, a))
+    assert same(qp, qd) and same(rp, rd)
+    e = config2_eigh(batch=5500, n=64, seed=39)
+    wp, vp, ip = api.eigh(cuda.from_numpy(e).pin_memory())
+    wd, vd, idv = api.eigh(dev(cuda, e))
+    assert same(wp, wd) and same(vp, vd) and np.array_equal(u32(ip), u32(idv))
