@@ -284,17 +284,31 @@ __device__ __forceinline__ void load_symmetric(float (&x)[N], EighLds<N>& s, con
         // a lane outside the read triangle reads row r's diagonal entry in
         // place of its own (the value is replaced below): only the read
         // triangle's cache lines are fetched
-        // a buffer resource over the group's matrix: SGPR base, 32-bit
-        // byte offsets per lane, the row's offset an immediate
-        const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, N * N * 4, 0x00020000);
-        const int cb = 4 * c;
+        if constexpr (N == 64) {
+            // one matrix per wave: a buffer resource over it (SGPR base,
+            // 32-bit offsets per lane, the row's offset an immediate)
+            // (the base made uniform explicitly: otherwise the compiler
+            // wraps every load in a loop over the distinct bases)
+            const uint64_t pv = reinterpret_cast<uint64_t>(src);
+            const uint32_t plo = __builtin_amdgcn_readfirstlane((uint32_t)pv);
+            const uint32_t phi = __builtin_amdgcn_readfirstlane((uint32_t)(pv >> 32));
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                reinterpret_cast<float*>(((uint64_t)phi << 32) | plo), (short)0, N * N * 4, 0x00020000);
+            const int cb = 4 * c;
 #pragma unroll
-        for (int r = 0; r < N; ++r) {
-            const int vo = 4 * N * r + (LOWER ? min(cb, 4 * r) : max(cb, 4 * r));
-            x[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, 0, 0));
-            // 16 loads at a time: their addresses are not all held at once
-            if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+            for (int r = 0; r < N; ++r) {
+                const int vo = 4 * N * r + (LOWER ? min(cb, 4 * r) : max(cb, 4 * r));
+                x[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, vo, 0, 0));
+                if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            // several matrices per wave: the base differs between lane
+            // groups (a buffer resource must be uniform), so global loads
+#pragma unroll
+            for (int r = 0; r < N; ++r) {
+                x[r] = src[r * N + (LOWER ? min(c, r) : max(c, r))];
+                if ((r & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+            }
         }
     } else {
         const int cc = c < nn ? c : nn - 1;
