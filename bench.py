@@ -525,6 +525,57 @@ def cpu_baseline(wl, host, seconds):
                       f"{host_cpus()}; {oracle.config()}"}
 
 
+# The other BASELINE configs, timed in the default run beside the headline
+# (device pointers through the C ABI, as the headline's steps): config 1,
+# config 3, config 4's four calls and config 5's four 4096 x 4096 calls.
+OTHER_CONFIGS = [("qr", 20), ("svd", 10), ("cholesky", 20), ("lu", 20), ("solve", 20), ("trsm", 20),
+                 ("cholesky4096", 5), ("lu4096", 3), ("qr4096", 3), ("eigh4096", 2)]
+
+
+def other_configs(_lib, skip):
+    """{workload: rate, time per call and roofline fraction} for the configs
+    other than `skip`; each one's failure is reported in its entry."""
+    import torch
+
+    out = {}
+    for name, steps in OTHER_CONFIGS:
+        if name == skip:
+            continue
+        try:
+            wl = workloads()[name]
+            dev = {k: torch.from_numpy(np.ascontiguousarray(v)).to("cuda") for k, v in wl.make().items()}
+            cabi = CAbi(_lib)
+            cabi.allocate(wl, dev)
+            wl.call(cabi, dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                wl.call(cabi, dev)
+            torch.cuda.synchronize()
+            elapsed = time.perf_counter() - t0
+            names = wl.kernel if isinstance(wl.kernel, (list, tuple)) else [wl.kernel]
+            _lib.hip_reset_timing()
+            _lib.hip_set_timing(1)
+            for _ in range(steps):
+                wl.call(cabi, dev)
+            torch.cuda.synchronize()
+            _lib.hip_set_timing(0)
+            kernel_s = sum(_lib.kernel_time(k)[1] for k in names) / 1e3 / steps
+            if wl.bound == "hbm":
+                frac = wl.bytes_per_call / kernel_s / 1e9 / HBM_PEAK_GBS
+            else:
+                frac = wl.flops_per_call / kernel_s / 1e12 / FP32_MFMA_PEAK_TFS
+            out[name] = {"value": round(wl.rate(steps, elapsed), 2), "unit": wl.unit,
+                         "ms_per_call": round(elapsed * 1e3 / steps, 4),
+                         "kernel_us_per_call": round(kernel_s * 1e6, 2), "roofline_bound": wl.bound,
+                         "roofline_frac": round(frac, 5), "steps": steps}
+            del dev, cabi
+        except Exception as e:   # reported, not fatal: the headline line is printed regardless
+            out[name] = {"error": f"{type(e).__name__}: {e}"}
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -535,6 +586,8 @@ def main():
     ap.add_argument("--no-host-path", action="store_true",
                     help="skip the host-pointer leg (for profiler runs that count only the device calls)")
     ap.add_argument("--cpu-seconds", type=float, default=2.0, help="wall seconds of the CPU baseline sample")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip timing the other BASELINE configs (they run by default beside the headline)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -631,6 +684,12 @@ def main():
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(wl, host, args.cpu_seconds)
 
+    # the other configs, in the default run only (a profiler run names its
+    # workload and skips the host path)
+    others = None
+    if not args.no_other_configs and not args.no_host_path and args.workload == "eigh":
+        others = other_configs(_lib, wl.name)
+
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -652,6 +711,7 @@ def main():
         "host_pointer_rate": host_path["value"] if host_path else None,
         "host_pointer": host_path,
         "kernels": {k: {"launches": v[0], "total_ms": round(v[1], 4)} for k, v in other.items()},
+        "other_configs": others,
         "device": _lib.device_name().decode(),
         "arch": _lib.hip_arch().decode(),
     }
