@@ -557,19 +557,20 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
 #pragma unroll
             for (int i = 0; i < kRB; ++i) {
                 const float* v = w + W.refl() + (size_t)max(kb - i, 0) * M;
-                const float p0 = v[c0], p1 = v[c1];
-                n0[i] = c < M ? p0 : 0.0f;
-                n1[i] = c + 64 < M ? p1 : 0.0f;
+                // raw values: masked when staged, a block later (a select
+                // here would wait for the loads at once)
+                n0[i] = v[c0];
+                n1[i] = v[c1];
             }
-            tn = c < kRB ? w[W.tq() + max(kb - c, 0)] : 0.0f;
+            tn = w[W.tq() + max(kb - min(c, kRB - 1), 0)];   // stored by lanes c < kRB only
         };
         fetch(N - 1);
         for (int kb = N - 1, blk = 0; kb >= 0; kb -= kRB, ++blk) {
             float(*vk)[kMaxM] = sb.v[blk & 1];
 #pragma unroll
             for (int i = 0; i < kRB; ++i) {
-                vk[i][c] = n0[i];
-                vk[i][c + 64] = n1[i];
+                vk[i][c] = c < M ? n0[i] : 0.0f;
+                vk[i][c + 64] = c + 64 < M ? n1[i] : 0.0f;
             }
             if (c < kRB) sb.tau[blk & 1][c] = tn;
             if (kb - kRB >= 0) fetch(kb - kRB);
@@ -625,16 +626,15 @@ __global__ __launch_bounds__(64) void svd_backtransform_kernel(const float* __re
         auto fetch = [&](int kb) {
 #pragma unroll
             for (int i = 0; i < kRB; ++i) {
-                const float p0 = w[W.refr() + (size_t)max(kb - i, 0) * N + cc];
-                n0[i] = c < N ? p0 : 0.0f;
+                n0[i] = w[W.refr() + (size_t)max(kb - i, 0) * N + cc];   // masked when staged
             }
-            tn = c < kRB ? w[W.tp() + max(kb - c, 0)] : 0.0f;
+            tn = w[W.tp() + max(kb - min(c, kRB - 1), 0)];
         };
         fetch(N - 2);
         for (int kb = N - 2, blk = 0; kb >= 0; kb -= kRB, ++blk) {
             float(*uk)[kMaxM] = sb.v[blk & 1];
 #pragma unroll
-            for (int i = 0; i < kRB; ++i) uk[i][c] = n0[i];
+            for (int i = 0; i < kRB; ++i) uk[i][c] = c < N ? n0[i] : 0.0f;
             if (c < kRB) sb.tau[blk & 1][c] = tn;
             if (kb - kRB >= 0) fetch(kb - kRB);
             __syncthreads();
