@@ -543,15 +543,19 @@ __global__ __launch_bounds__(kThreads) void eigh_mid_values_kernel(const float* 
 // from V's storage in blocks of kBT (thread c loads element c of each, one
 // block ahead), staged in LDS and read as broadcasts; entries at and above
 // row K are zero.
-__device__ __forceinline__ void bt_fetch(float (&nx)[kBT], const float* vg, int kb, int c, int n) {
+// The loads are masked only when the block is staged, a block later: a
+// select right after them would wait for them.
+__device__ __forceinline__ int bt_k(int kb, int i, int n) {
     const int kmax = n - 3;
+    return kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
+}
+__device__ __forceinline__ void bt_fetch(float (&nx)[kBT], const float* vg, int kb, int c, int n) {
 #pragma unroll
     for (int i = 0; i < kBT; ++i) {
-        const int k = kb - i < 0 ? 0 : (kb - i > kmax ? kmax : kb - i);
+        const int k = bt_k(kb, i, n);
         const bool in = c > k && c < n;
         const int off = refl_offset(k, n);
-        const float v = vg[in ? off + c - k - 1 : off];
-        nx[i] = in ? v : 0.0f;
+        nx[i] = vg[in ? off + c - k - 1 : off];
     }
 }
 
@@ -566,7 +570,10 @@ __device__ __forceinline__ void bt_phase(float (&x)[kC * MC], MidLds& s, int c, 
         const int blk = q / kBT, i = q - blk * kBT;
         if (i == 0) {   // a new block: store the fetched one, fetch the next
 #pragma unroll
-            for (int j = 0; j < kBT; ++j) s.bt[blk & 1][j][c] = nx[j];
+            for (int j = 0; j < kBT; ++j) {
+                const int k = bt_k(K, j, n);
+                s.bt[blk & 1][j][c] = (c > k && c < n) ? nx[j] : 0.0f;
+            }
             if (K - kBT >= 0) bt_fetch(nx, vg, K - kBT, c, n);
             __syncthreads();
         }
